@@ -1,0 +1,143 @@
+/*
+ * kvhip.h - C ABI of the MI355X (gfx950) paged-attention backend for kvserve.
+ *
+ * Plain C: pointers, sizes and int64 strides only; no torch or HIP types cross this
+ * boundary (a stream is passed as the opaque hipStream_t handle, typed void*).
+ * Every entry point is reentrant, allocates no device memory, never synchronises the
+ * stream and never throws: failures come back as a status code.
+ *
+ * Status codes: 0 = OK, < 0 = invalid argument (see KVH_E_*), > 0 = hipError_t of a
+ * failed launch. kvh_strerror() turns either kind into text.
+ *
+ * Element types (KVH_DTYPE_*) select the storage type of q, k, v, the caches and out.
+ * bf16/fp16 use the MFMA kernels (fp32 accumulation); fp32 uses exact fp32 FMA.
+ *
+ * Tensor conventions (all strides in ELEMENTS, last dim contiguous):
+ *   q, out             [num_tokens, num_heads, head_dim]   flat token batch
+ *   k, v (new tokens)  [num_tokens, num_kv_heads, head_dim]
+ *   k_cache, v_cache   [num_blocks, block_size, num_kv_heads, head_dim]
+ *                      cache_strides = {block, slot, head}
+ *   block_tables       int64 [num_seqs, row_stride], first max_blocks_per_seq used
+ *   seq_lens           int64 [num_seqs]  context length INCLUDING this step's tokens
+ *   query_start_loc    int64 [num_seqs + 1] prefix sums of per-sequence query lengths
+ *   slot_mapping       int64 [num_tokens] flat slot = block * block_size + offset
+ */
+#ifndef KVHIP_H
+#define KVHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVH_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define KVH_API __attribute__((visibility("default")))
+#else
+#define KVH_API
+#endif
+
+enum kvh_dtype {
+  KVH_DTYPE_F32 = 0,
+  KVH_DTYPE_F16 = 1,
+  KVH_DTYPE_BF16 = 2,
+};
+
+enum kvh_status {
+  KVH_OK = 0,
+  KVH_E_NULL = -1,        /* a required pointer is NULL */
+  KVH_E_SHAPE = -2,       /* a size is out of range or inconsistent */
+  KVH_E_DTYPE = -3,       /* unknown dtype */
+  KVH_E_ALIGN = -4,       /* pointer/stride not aligned for the vector kernels */
+  KVH_E_UNSUPPORTED = -5, /* valid, but not a head_dim/block_size/GQA combination built here */
+  KVH_E_WORKSPACE = -6,   /* workspace missing or smaller than kvh_paged_attention_workspace_size() */
+};
+
+/* ABI version this library was built with (KVH_ABI_VERSION). */
+KVH_API int kvh_abi_version(void);
+
+/* Static text for a status code (negative: argument errors, positive: hipError_t). */
+KVH_API const char* kvh_strerror(int status);
+
+/*
+ * reshape_and_cache: scatter this step's K/V rows into the paged pool.
+ *   k_cache[slot / block_size, slot % block_size, h, :] = k[t, h, :]   (same for v)
+ * with slot = slot_mapping[t]. k and v may have any token/head stride (v is usually a
+ * strided view of the fused QKV output). Duplicate slots are allowed (CUDA-graph padding
+ * rows all write the scratch slot); which duplicate wins is unspecified, as with the
+ * reference. Slots outside [0, num_blocks * block_size) are skipped.
+ *
+ * Replaces TorchAttention.write_kv, src/kvserve/attention.py:39-45 (two index_put_ scatters).
+ */
+KVH_API int kvh_reshape_and_cache(const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                          const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                          void* k_cache, const int64_t k_cache_strides[3],
+                          void* v_cache, const int64_t v_cache_strides[3],
+                          const int64_t* slot_mapping, int64_t num_tokens, int64_t num_blocks,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                          int32_t dtype, void* stream);
+
+/*
+ * Bytes of device workspace kvh_paged_attention needs for this launch shape. Depends only
+ * on static quantities (shapes, the block-table width and max_query_len), so a CUDA/HIP
+ * graph can allocate it once at capture. May return 0.
+ */
+KVH_API size_t kvh_paged_attention_workspace_size(int64_t num_tokens, int32_t num_seqs, int32_t num_heads,
+                                          int32_t num_kv_heads, int32_t head_dim,
+                                          int32_t max_blocks_per_seq, int32_t block_size,
+                                          int32_t max_query_len, int32_t dtype);
+
+/*
+ * Paged attention over a flat batch that mixes decode tokens and prefill chunks.
+ * For query token i of sequence s (absolute position ctx + i, ctx = seq_len - q_len) and
+ * head h (kv head h / (num_heads / num_kv_heads)):
+ *   out[t, h] = softmax_j(scale * q[t, h] . K[j]) V[j],  j = 0 .. ctx + i   (causal)
+ * with K/V read at cache[block_tables[s, j / block_size], j % block_size, h_kv].
+ * A row with no visible key writes zeros.
+ *
+ * max_query_len must bound every sequence's query length (host int, as in the reference);
+ * max_blocks_per_seq is the block-table width W (static under graph capture). Only the
+ * first ceil(seq_len / block_size) table entries of a row are read; ids outside
+ * [0, num_blocks) are treated as empty pages. The call does not depend on max_seq_len.
+ *
+ * Replaces paged_attention(), src/kvserve/kernels/paged_attention.py:118-157, as called by
+ * TritonAttention.forward, src/kvserve/attention.py:88-102.
+ */
+KVH_API int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                        const void* k_cache, const int64_t k_cache_strides[3],
+                        const void* v_cache, const int64_t v_cache_strides[3],
+                        int64_t num_blocks,
+                        void* out, int64_t o_tok_stride, int64_t o_head_stride,
+                        const int64_t* block_tables, int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                        const int64_t* seq_lens, const int64_t* query_start_loc,
+                        int64_t num_tokens, int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t block_size, int32_t max_query_len, float scale,
+                        int32_t dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Launch-timing hook for benchmarks (no counterpart in the reference). When armed with an
+ * array of n <= 8 hipEvent_t handles (created by the caller with timing enabled), the NEXT
+ * kvh_paged_attention call on this host thread records events[0] on its stream before its
+ * first kernel and events[k] right after its k-th kernel (k = 1 .. n-1), then disarms
+ * itself. The call still launches all of its work. Pass events = NULL to disarm.
+ */
+KVH_API int kvh_profile_arm(void* const* events, int32_t num_events);
+
+/* Kernels launched by the last kvh_paged_attention call on this thread, in launch order:
+ * writes up to cap kernel-kind codes (KVH_KERNEL_*) and returns how many there were. */
+enum kvh_kernel_kind {
+  KVH_KERNEL_DECODE = 1,   /* split-K decode-class partitions (q_len small) */
+  KVH_KERNEL_PREFILL = 2,  /* prefill/verify-class tiles (q_len large) */
+  KVH_KERNEL_REDUCE = 3,   /* log-sum-exp merge of decode partitions */
+  KVH_KERNEL_F32 = 4,      /* exact fp32 path */
+};
+KVH_API int kvh_last_launch_kernels(int32_t* kinds, int32_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVHIP_H */

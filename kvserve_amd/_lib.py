@@ -1,0 +1,101 @@
+"""ctypes binding of libkvhip.so (the C ABI declared in include/kvhip.h).
+
+torch is imported first on purpose: torch ships its own HIP runtime (libamdhip64.so.7),
+and loading it before libkvhip makes the library bind to that same runtime instance,
+so the hipStream_t handles torch hands out are valid inside the library.
+
+There is no fallback: if the library is missing or fails to load, every entry point
+raises. Build it with `python -m kvserve_amd.build`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (see module docstring: must precede the CDLL load)
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libkvhip.so"
+
+ABI_VERSION = 1
+
+KVH_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+KERNEL_KINDS = {1: "decode", 2: "prefill", 3: "reduce", 4: "f32"}
+
+_i32, _i64, _f32, _vp, _sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+# name -> (restype, argtypes), in the order of include/kvhip.h
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "kvh_abi_version": (ctypes.c_int, []),
+    "kvh_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+    "kvh_reshape_and_cache": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64p, _vp, _i64p, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "kvh_paged_attention_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "kvh_paged_attention": (
+        ctypes.c_int,
+        [
+            _vp, _i64, _i64,  # q
+            _vp, _i64p, _vp, _i64p, _i64,  # caches, num_blocks
+            _vp, _i64, _i64,  # out
+            _vp, _i64, _i32,  # block tables
+            _vp, _vp,  # seq_lens, query_start_loc
+            _i64, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32,  # sizes, scale, dtype
+            _vp, _sz, _vp,  # workspace, stream
+        ],  # fmt: skip
+    ),
+    "kvh_profile_arm": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), _i32]),
+    "kvh_last_launch_kernels": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int32), _i32]),
+}
+
+_lib: ctypes.CDLL | None = None
+_lock = threading.Lock()
+
+
+class KvhError(RuntimeError):
+    """A nonzero status from libkvhip (argument error or failed HIP launch)."""
+
+    def __init__(self, status: int, where: str):
+        self.status = status
+        super().__init__(f"{where}: {strerror(status)} (status {status})")
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raises RuntimeError when it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: the HIP backend has no fallback. Build it with `python -m kvserve_amd.build`."
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        version = lib.kvh_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"libkvhip ABI {version} does not match the Python binding ({ABI_VERSION})")
+        _lib = lib
+    return _lib
+
+
+def strerror(status: int) -> str:
+    return load().kvh_strerror(status).decode()
+
+
+def check(status: int, where: str) -> None:
+    if status != 0:
+        raise KvhError(status, where)
+
+
+def i64x3(values) -> ctypes.Array:
+    return (ctypes.c_int64 * 3)(*[int(v) for v in values])

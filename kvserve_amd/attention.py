@@ -1,0 +1,240 @@
+"""kvserve's attention-backend interface, served by the gfx950 HIP kernels.
+
+Mirrors src/kvserve/attention.py of the reference:
+  * `AttentionMetadata` has the same fields and meaning (attention.py:17-28);
+  * `HipAttention` is a class used as a namespace of static methods with the exact
+    `write_kv` / `forward` signatures of the reference's backends (attention.py:39-82,
+    :88-102), so `Attention.attend` (model.py:96-108) calls it unchanged;
+  * `get_backend(name, device, block_size)` keeps the reference's selector contract
+    (attention.py:113-124) for the names this package serves ("hip", "auto").
+
+Both methods run on `torch.cuda.current_stream()`, allocate only through torch's caching
+allocator (the output when `out is None`, and the split-K workspace), never synchronise
+and never read `meta.max_seq_len`, so they can be captured in a HIP graph (the decode
+graph of cuda_graph.py:79-102) and called between piecewise-graph replays
+(cuda_graph.py:234-240).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from kvserve_amd import _lib
+
+
+@dataclass
+class AttentionMetadata:
+    """Same fields as the reference's AttentionMetadata (src/kvserve/attention.py:17-28)."""
+
+    slot_mapping: torch.Tensor  # [T] flat KV slot for each new token
+    block_tables: torch.Tensor  # [B, max_blocks] physical block ids, 0-padded
+    seq_lens: torch.Tensor  # [B] context length including this step's tokens
+    query_lens: torch.Tensor  # [B] tokens computed this step
+    query_start_loc: torch.Tensor  # [B + 1] offset of each sequence's first token in the flat batch
+    max_seq_len: int
+    max_query_len: int
+    # Padded layout, needed only by the reference's torch backend; never read here.
+    q_gather: torch.Tensor | None = None
+    q_valid: torch.Tensor | None = None
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _dtype_code(*tensors: torch.Tensor) -> int:
+    dt = tensors[0].dtype
+    _require(all(t.dtype == dt for t in tensors), f"dtype mismatch: {[t.dtype for t in tensors]}")
+    _require(dt in _lib.KVH_DTYPE, f"unsupported dtype {dt} (float32, float16, bfloat16)")
+    return _lib.KVH_DTYPE[dt]
+
+
+def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+    _require(k_cache.dim() == 4 and k_cache.shape == v_cache.shape, "caches must be [num_blocks, block_size, kv_heads, D]")
+    _require(k_cache.stride(-1) == 1 and v_cache.stride(-1) == 1, "cache last dim must be contiguous")
+    _require(k_cache.is_cuda and v_cache.is_cuda, "caches must be on a HIP device")
+
+
+def _check_index(t: torch.Tensor, name: str, dim: int) -> None:
+    _require(t.dtype == torch.int64, f"{name} must be int64 (got {t.dtype})")
+    _require(t.is_cuda, f"{name} must be on the device")
+    _require(t.dim() == dim and t.stride(-1) == 1, f"{name} must be {dim}-d with a contiguous last dim")
+
+
+class HipAttention:
+    """Paged attention on hand-written gfx950 kernels (decode split-K + reduce, MFMA prefill).
+
+    Drop-in for the reference's TritonAttention (src/kvserve/attention.py:85-102): same
+    static methods, same arguments, same return value.
+    """
+
+    name = "hip"
+    # Capabilities the reference's ModelRunner expresses as `backend is TritonAttention`
+    # identity checks (model_runner.py:45,47,190).
+    graph_capturable = True  # decode and piecewise graphs may capture it
+    needs_padded_layout = False  # never reads meta.q_gather / meta.q_valid
+    needs_warmup = False  # ahead-of-time compiled: nothing to JIT (model_runner.py:62-89)
+
+    @staticmethod
+    def write_kv(
+        k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor
+    ) -> None:
+        """reshape_and_cache: cache.view(-1, Hkv, D)[slots] = k (and v), bit for bit.
+
+        caches: [num_blocks, block_size, kv_heads, head_dim]; k, v: [T, kv_heads, head_dim],
+        any token/head stride (v is typically a strided view of the fused QKV output).
+        Slots outside the pool are skipped instead of raising.
+        """
+        _check_cache(k_cache, v_cache)
+        num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
+        _require(k.dim() == 3 and k.shape == v.shape, "k and v must be [T, kv_heads, head_dim]")
+        _require(k.shape[1:] == (num_kv_heads, head_dim), f"k/v rows {tuple(k.shape[1:])} != cache rows")
+        _require(k.stride(-1) == 1 and v.stride(-1) == 1, "k/v last dim must be contiguous")
+        _check_index(slots, "slot_mapping", 1)
+        _require(slots.shape[0] == k.shape[0], "one slot per token")
+        dtype = _dtype_code(k_cache, v_cache, k, v)
+        lib = _lib.load()
+        st = lib.kvh_reshape_and_cache(
+            k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+            k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(), _lib.i64x3(v_cache.stride()[:3]),
+            slots.data_ptr(), k.shape[0], num_blocks, num_kv_heads, head_dim, block_size, dtype,
+            _stream_handle(k_cache.device),
+        )  # fmt: skip
+        _lib.check(st, "kvh_reshape_and_cache")
+
+    @staticmethod
+    def forward(
+        q: torch.Tensor,
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor,
+        meta: AttentionMetadata,
+        scale: float,
+        out: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """q: [T, H, D]; caches: [num_blocks, block_size, H_kv, D]. Returns [T, H, D] (in `out` if given)."""
+        _check_cache(k_cache, v_cache)
+        num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
+        _require(q.dim() == 3 and q.shape[2] == head_dim, "q must be [T, H, head_dim]")
+        _require(q.stride(-1) == 1, "q last dim must be contiguous")
+        num_tokens, num_heads, _ = q.shape
+        _require(num_heads % num_kv_heads == 0, "num_heads must be a multiple of num_kv_heads")
+        tables, seq_lens, qsl = meta.block_tables, meta.seq_lens, meta.query_start_loc
+        _check_index(tables, "block_tables", 2)
+        _check_index(seq_lens, "seq_lens", 1)
+        _check_index(qsl, "query_start_loc", 1)
+        num_seqs = tables.shape[0]
+        _require(seq_lens.shape[0] == num_seqs and qsl.shape[0] == num_seqs + 1, "metadata sizes disagree")
+        if out is None:
+            out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        _require(out.shape == q.shape and out.stride(-1) == 1, "out must match q with a contiguous last dim")
+        dtype = _dtype_code(q, k_cache, v_cache, out)
+        if num_tokens == 0 or num_seqs == 0:
+            return out
+        lib = _lib.load()
+        width = tables.shape[1]
+        max_q = int(meta.max_query_len)
+        ws_bytes = lib.kvh_paged_attention_workspace_size(
+            num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, width, block_size, max_q, dtype
+        )
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+        st = lib.kvh_paged_attention(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(), _lib.i64x3(v_cache.stride()[:3]),
+            num_blocks,
+            out.data_ptr(), out.stride(0), out.stride(1),
+            tables.data_ptr(), tables.stride(0), width,
+            seq_lens.data_ptr(), qsl.data_ptr(),
+            num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_q, float(scale), dtype,
+            ws.data_ptr() if ws is not None else None, ws_bytes, _stream_handle(q.device),
+        )  # fmt: skip
+        _lib.check(st, "kvh_paged_attention")
+        return out
+
+
+def last_launch_kernels() -> list[str]:
+    """Kernel kinds launched by the last forward() on this thread, in order."""
+    buf = (ctypes.c_int32 * 8)()
+    n = _lib.load().kvh_last_launch_kernels(buf, 8)
+    return [_lib.KERNEL_KINDS.get(buf[i], "?") for i in range(min(n, 8))]
+
+
+def hip_available() -> bool:
+    """True when a ROCm build of torch sees a GPU and libkvhip loads."""
+    if torch.version.hip is None or not torch.cuda.is_available():
+        return False
+    try:
+        _lib.load()
+    except (RuntimeError, OSError):
+        return False
+    return True
+
+
+def get_backend(name: str, device: str, block_size: int) -> type[HipAttention]:
+    """Selector with the reference's contract (src/kvserve/attention.py:113-124).
+
+    "hip" (and "auto" on a ROCm device) -> HipAttention. The reference's "torch" and
+    "triton" names stay with the reference's own classes; this package does not ship a
+    CPU path. Errors mirror the reference: RuntimeError when the backend cannot run,
+    ValueError for an unsupported block size or an unknown name.
+    """
+    if name == "auto":
+        if not (device.startswith("cuda") and hip_available()):
+            raise RuntimeError("auto: no ROCm GPU + libkvhip here; select kvserve's own 'torch' backend instead")
+        name = "hip"
+    if name == "hip":
+        if not hip_available():
+            raise RuntimeError("hip backend needs a ROCm GPU and a built kvserve_amd/lib/libkvhip.so")
+        if block_size < 16 or block_size % 16 != 0:
+            raise ValueError("hip backend needs block_size a multiple of 16 (16-token MFMA tiles)")
+        return HipAttention
+    if name in ("torch", "triton"):
+        raise ValueError(f"backend {name!r} belongs to kvserve.attention; kvserve_amd serves 'hip' and 'auto'")
+    raise ValueError(f"unknown attention backend {name!r}")
+
+
+def build_metadata(
+    device: torch.device | str,
+    block_tables: list[list[int]],
+    slots: list[int],
+    seq_lens: list[int],
+    query_lens: list[int],
+    padded_layout: bool = False,
+) -> AttentionMetadata:
+    """Metadata for a flat batch where sequence i contributes query_lens[i] tokens.
+
+    Same layout and dtypes as the reference's build_metadata (src/kvserve/model_runner.py:165-197):
+    int64 tensors, block tables 0-padded to the longest row, query_start_loc prefix sums.
+    The padded q_gather / q_valid tensors are built only when `padded_layout` is set
+    (the reference keys this on `backend is not TritonAttention`, :190).
+    """
+    max_blocks = max(len(t) for t in block_tables)
+    tables = [t + [0] * (max_blocks - len(t)) for t in block_tables]
+    max_q = max(query_lens)
+    query_start_loc = [0]
+    for n in query_lens:
+        query_start_loc.append(query_start_loc[-1] + n)
+    meta = AttentionMetadata(
+        slot_mapping=torch.tensor(slots, dtype=torch.long, device=device),
+        block_tables=torch.tensor(tables, dtype=torch.long, device=device),
+        seq_lens=torch.tensor(seq_lens, dtype=torch.long, device=device),
+        query_lens=torch.tensor(query_lens, dtype=torch.long, device=device),
+        query_start_loc=torch.tensor(query_start_loc, dtype=torch.long, device=device),
+        max_seq_len=max(seq_lens),
+        max_query_len=max_q,
+    )
+    if padded_layout:
+        q_gather, q_valid = [], []
+        for start, n in zip(query_start_loc, query_lens):
+            q_gather.append(list(range(start, start + n)) + [0] * (max_q - n))
+            q_valid.append([True] * n + [False] * (max_q - n))
+        meta.q_gather = torch.tensor(q_gather, dtype=torch.long, device=device)
+        meta.q_valid = torch.tensor(q_valid, dtype=torch.bool, device=device)
+    return meta

@@ -1,0 +1,90 @@
+"""Build libkvhip.so (the gfx950 kernels + C ABI) in-tree with hipcc.
+
+    python -m kvserve_amd.build            # compile every source, link kvserve_amd/lib/libkvhip.so
+
+Objects go to kvserve_amd/_build/, the library to kvserve_amd/lib/. Both are git-ignored
+build products; the library travels with the source tree so a GPU host needs no compiler.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB_DIR = PKG / "lib"
+LIB = LIB_DIR / "libkvhip.so"
+INCLUDE = PKG.parent / "include"
+
+SOURCES = ["kvh_api.hip", "paged_attention.hip", "paged_attention_f32.hip", "reshape_and_cache.hip"]
+
+# -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32 (unreliable on these
+# hosts); the host pass warns that it does not know the feature, which is harmless.
+HIP_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(exe).exists():
+        raise RuntimeError("hipcc not found: libkvhip.so cannot be built")
+    return exe
+
+
+def _run(cmd: list[str]) -> None:
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in (res.stdout + res.stderr).splitlines() if noise not in line)
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
+    """Compile all sources (always; no staleness check) and link the shared library."""
+    BUILD.mkdir(exist_ok=True)
+    LIB_DIR.mkdir(exist_ok=True)
+    cc = hipcc()
+    flags = HIP_FLAGS + list(extra_flags or [])
+
+    def compile_one(src: str) -> Path:
+        obj = BUILD / (Path(src).stem + ".o")
+        cmd = [cc, *flags, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd))
+        _run(cmd)
+        return obj
+
+    jobs = min(len(SOURCES), int(os.environ.get("MAX_JOBS", "8")), 16)
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        objs = list(ex.map(compile_one, SOURCES))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [cc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    if verbose:
+        print(" ".join(cmd))
+    _run(cmd)
+    os.replace(tmp, LIB)  # atomic: a process that already mapped the old file keeps it
+    return LIB
+
+
+if __name__ == "__main__":
+    path = build(verbose="-v" in sys.argv)
+    print(path)

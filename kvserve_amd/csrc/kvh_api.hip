@@ -1,0 +1,277 @@
+// C ABI of libkvhip: argument validation, the static launch plan and dispatch.
+// Host code only; kernels live in paged_attention*.hip and reshape_and_cache.hip.
+#include <stdlib.h>
+#include <string.h>
+
+#include "../../include/kvhip.h"
+#include "kvh_device.h"
+#include "kvh_internal.h"
+
+namespace kvh {
+
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int elem_bytes(int dtype) { return dtype == KVH_DTYPE_F32 ? 4 : 2; }
+
+// Launch-timing state of this host thread (see kvh_profile_arm).
+struct ProfileState {
+  void* events[8] = {nullptr};
+  int32_t num_events = 0;
+  int32_t last_kinds[8] = {0};
+  int32_t last_count = 0;
+};
+thread_local ProfileState g_prof;
+
+// Tokens per split-K partition; KVH_PARTITION_TOKENS (a multiple of 128) overrides the
+// heuristic, for tuning sweeps.
+int partition_override() {
+  static int v = [] {
+    const char* s = getenv("KVH_PARTITION_TOKENS");
+    int x = s ? atoi(s) : 0;
+    return (x >= 128 && x % 128 == 0) ? x : 0;
+  }();
+  return v;
+}
+
+}  // namespace
+
+void LaunchLog::after_launch(int kind, hipStream_t s) {
+  if (launched < 8) kinds[launched] = kind;
+  ++launched;
+  if (events && launched < num_events && events[launched]) (void)hipEventRecord((hipEvent_t)events[launched], s);
+}
+
+Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t W, int32_t BS, int32_t max_q,
+               int32_t dtype) {
+  Plan pl{};
+  pl.G = H / Hkv;
+  if (max_q < 1) max_q = 1;
+  const int G = pl.G;
+  if ((int64_t)max_q * G <= 64) {
+    // decode / speculative-verify batch: every sequence takes the split-K kernel
+    pl.QS = max_q;
+    pl.launch_prefill = false;
+  } else {
+    // mixed batch: single-tile rows split-K, everything longer on the prefill kernel
+    pl.QS = G >= 16 ? 1 : 16 / G;
+    pl.launch_prefill = true;
+  }
+  pl.NT = (pl.QS * G + 15) / 16;
+  pl.pre_rows_per_wg = 128;
+  pl.pre_tiles = (int32_t)(((int64_t)max_q * G + pl.pre_rows_per_wg - 1) / pl.pre_rows_per_wg);
+  const int64_t max_keys = (int64_t)W * BS;
+  int ps = partition_override();
+  if (!ps) {
+    // Smallest partition (>= 128 tokens = one 32-token chunk per wave) that keeps the grid
+    // near 8K workgroups: enough to fill 256 CUs several times over while keeping the
+    // partial-result traffic a few percent of the KV bytes.
+    ps = 128;
+    while (ps < max_keys && (int64_t)B * Hkv * ((max_keys + ps - 1) / ps) > 8192) ps *= 2;
+  }
+  pl.PS = ps;
+  pl.P = (int32_t)((max_keys + ps - 1) / ps);
+  if (pl.P < 1) pl.P = 1;
+  if (dtype == KVH_DTYPE_F32 || pl.P == 1) {
+    pl.ws_acc_bytes = pl.ws_ml_bytes = pl.ws_bytes = 0;
+  } else {
+    pl.ws_acc_bytes = align_up((size_t)T * H * pl.P * D * sizeof(float));
+    pl.ws_ml_bytes = align_up((size_t)T * H * pl.P * 2 * sizeof(float));
+    pl.ws_bytes = pl.ws_acc_bytes + pl.ws_ml_bytes;
+  }
+  return pl;
+}
+
+}  // namespace kvh
+
+using namespace kvh;
+
+extern "C" {
+
+int kvh_abi_version(void) { return KVH_ABI_VERSION; }
+
+const char* kvh_strerror(int status) {
+  switch (status) {
+    case KVH_OK: return "ok";
+    case KVH_E_NULL: return "kvhip: a required pointer is NULL";
+    case KVH_E_SHAPE: return "kvhip: size out of range or inconsistent";
+    case KVH_E_DTYPE: return "kvhip: unknown dtype";
+    case KVH_E_ALIGN: return "kvhip: pointer or stride not aligned (16-byte rows required)";
+    case KVH_E_UNSUPPORTED: return "kvhip: unsupported head_dim / block_size / GQA combination";
+    case KVH_E_WORKSPACE: return "kvhip: workspace missing or too small";
+    default: break;
+  }
+  if (status > 0) return hipGetErrorString((hipError_t)status);
+  return "kvhip: unknown status";
+}
+
+int kvh_reshape_and_cache(const void* k, int64_t k_tok_stride, int64_t k_head_stride, const void* v,
+                          int64_t v_tok_stride, int64_t v_head_stride, void* k_cache,
+                          const int64_t k_cache_strides[3], void* v_cache, const int64_t v_cache_strides[3],
+                          const int64_t* slot_mapping, int64_t num_tokens, int64_t num_blocks, int32_t num_kv_heads,
+                          int32_t head_dim, int32_t block_size, int32_t dtype, void* stream) {
+  if (dtype < KVH_DTYPE_F32 || dtype > KVH_DTYPE_BF16) return KVH_E_DTYPE;
+  if (num_tokens < 0 || num_blocks < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0)
+    return KVH_E_SHAPE;
+  if (num_tokens > 0x7fffffffLL) return KVH_E_SHAPE;
+  if (num_tokens == 0) return KVH_OK;
+  if (!k || !v || !k_cache || !v_cache || !k_cache_strides || !v_cache_strides || !slot_mapping) return KVH_E_NULL;
+  const int eb = elem_bytes(dtype);
+  const int64_t strides[] = {k_tok_stride, k_head_stride, v_tok_stride, v_head_stride,
+                             k_cache_strides[0], k_cache_strides[1], k_cache_strides[2],
+                             v_cache_strides[0], v_cache_strides[1], v_cache_strides[2]};
+  const int vec_elems = 16 / eb;
+  bool vec16 = (head_dim * eb) % 16 == 0 && aligned16(k) && aligned16(v) && aligned16(k_cache) && aligned16(v_cache);
+  for (int64_t s : strides) {
+    if (s < 0) return KVH_E_SHAPE;
+    vec16 = vec16 && s % vec_elems == 0;
+  }
+  const uintptr_t emask = (uintptr_t)eb - 1;
+  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)k_cache | (uintptr_t)v_cache) & emask) return KVH_E_ALIGN;
+  return launch_reshape_and_cache(k, k_tok_stride, k_head_stride, v, v_tok_stride, v_head_stride, k_cache,
+                                  k_cache_strides, v_cache, v_cache_strides, slot_mapping, num_tokens, num_blocks,
+                                  num_kv_heads, head_dim, block_size, eb, vec16, (hipStream_t)stream);
+}
+
+static int check_attention_shape(int64_t num_tokens, int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                 int32_t head_dim, int32_t max_blocks_per_seq, int32_t block_size, int32_t dtype) {
+  if (dtype < KVH_DTYPE_F32 || dtype > KVH_DTYPE_BF16) return KVH_E_DTYPE;
+  if (num_tokens < 0 || num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      block_size <= 0 || max_blocks_per_seq <= 0)
+    return KVH_E_SHAPE;
+  if (num_heads % num_kv_heads != 0) return KVH_E_SHAPE;
+  if (num_seqs > 65535 || num_heads > 65535 || num_tokens > 0x7fffffffLL) return KVH_E_UNSUPPORTED;
+  if ((int64_t)max_blocks_per_seq * block_size >= 0x7fffffffLL) return KVH_E_UNSUPPORTED;
+  if (dtype == KVH_DTYPE_F32) {
+    if (head_dim % 4 != 0 || head_dim > 256) return KVH_E_UNSUPPORTED;
+  } else {
+    if (head_dim != 64 && head_dim != 128) return KVH_E_UNSUPPORTED;
+    if (block_size % 16 != 0) return KVH_E_UNSUPPORTED;
+    // the split-K kernel keeps at most 4 tiles of 16 query rows in registers
+    if (num_heads / num_kv_heads > 64) return KVH_E_UNSUPPORTED;
+  }
+  return KVH_OK;
+}
+
+size_t kvh_paged_attention_workspace_size(int64_t num_tokens, int32_t num_seqs, int32_t num_heads,
+                                          int32_t num_kv_heads, int32_t head_dim, int32_t max_blocks_per_seq,
+                                          int32_t block_size, int32_t max_query_len, int32_t dtype) {
+  if (check_attention_shape(num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size,
+                            dtype) != KVH_OK)
+    return 0;
+  return make_plan(num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size,
+                   max_query_len, dtype)
+      .ws_bytes;
+}
+
+int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride, const void* k_cache,
+                        const int64_t k_cache_strides[3], const void* v_cache, const int64_t v_cache_strides[3],
+                        int64_t num_blocks, void* out, int64_t o_tok_stride, int64_t o_head_stride,
+                        const int64_t* block_tables, int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                        const int64_t* seq_lens, const int64_t* query_start_loc, int64_t num_tokens, int32_t num_seqs,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        int32_t max_query_len, float scale, int32_t dtype, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  // the timing hook covers exactly one call, whatever its outcome
+  LaunchLog log;
+  void* armed[8];
+  const int32_t n_armed = g_prof.num_events;
+  memcpy(armed, g_prof.events, sizeof(armed));
+  g_prof.num_events = 0;
+  g_prof.last_count = 0;
+
+  int st = check_attention_shape(num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
+                                 block_size, dtype);
+  if (st != KVH_OK) return st;
+  if (num_tokens == 0 || num_seqs == 0) return KVH_OK;
+  if (!q || !k_cache || !v_cache || !k_cache_strides || !v_cache_strides || !out || !block_tables || !seq_lens ||
+      !query_start_loc)
+    return KVH_E_NULL;
+  if (num_blocks < 0 || bt_row_stride < max_blocks_per_seq) return KVH_E_SHAPE;
+  const int64_t strides[] = {q_tok_stride, q_head_stride, o_tok_stride, o_head_stride,
+                             k_cache_strides[0], k_cache_strides[1], k_cache_strides[2],
+                             v_cache_strides[0], v_cache_strides[1], v_cache_strides[2]};
+  const int vec_elems = dtype == KVH_DTYPE_F32 ? 4 : 8;
+  for (int64_t s : strides) {
+    if (s < 0) return KVH_E_SHAPE;
+    if (s % vec_elems) return KVH_E_ALIGN;
+  }
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out)) return KVH_E_ALIGN;
+
+  const Plan plan = make_plan(num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size,
+                              max_query_len, dtype);
+  if (plan.ws_bytes > 0 && (!workspace || workspace_bytes < plan.ws_bytes || !aligned16(workspace)))
+    return KVH_E_WORKSPACE;
+
+  PAParams p{};
+  p.q = q;
+  p.q_ts = q_tok_stride;
+  p.q_hs = q_head_stride;
+  p.kc = k_cache;
+  p.k_sb = k_cache_strides[0];
+  p.k_ss = k_cache_strides[1];
+  p.k_sh = k_cache_strides[2];
+  p.vc = v_cache;
+  p.v_sb = v_cache_strides[0];
+  p.v_ss = v_cache_strides[1];
+  p.v_sh = v_cache_strides[2];
+  p.num_blocks = num_blocks;
+  p.out = out;
+  p.o_ts = o_tok_stride;
+  p.o_hs = o_head_stride;
+  p.bt = block_tables;
+  p.bt_rs = bt_row_stride;
+  p.seq_lens = seq_lens;
+  p.qsl = query_start_loc;
+  p.T = num_tokens;
+  p.W = max_blocks_per_seq;
+  p.B = num_seqs;
+  p.H = num_heads;
+  p.Hkv = num_kv_heads;
+  p.G = plan.G;
+  p.BS = block_size;
+  p.scale = scale;
+  p.qk_scale = scale * kLog2e;
+  p.QS = plan.QS;
+  p.PS = plan.PS;
+  p.P = plan.P;
+  p.ws_acc = plan.ws_bytes ? (float*)workspace : nullptr;
+  p.ws_ml = plan.ws_bytes ? (float*)((char*)workspace + plan.ws_acc_bytes) : nullptr;
+
+  hipStream_t s = (hipStream_t)stream;
+  if (n_armed > 0) {
+    log.events = armed;
+    log.num_events = n_armed;
+    if (armed[0]) (void)hipEventRecord((hipEvent_t)armed[0], s);
+  }
+  if (dtype == KVH_DTYPE_F32)
+    st = launch_paged_attention_f32(p, head_dim, max_query_len < 1 ? 1 : max_query_len, s, log);
+  else
+    st = launch_paged_attention_mfma(p, plan, head_dim, dtype, s, log);
+  g_prof.last_count = log.launched;
+  for (int i = 0; i < 8; ++i) g_prof.last_kinds[i] = log.kinds[i];
+  return st;
+}
+
+int kvh_profile_arm(void* const* events, int32_t num_events) {
+  if (!events || num_events <= 0) {
+    g_prof.num_events = 0;
+    return KVH_OK;
+  }
+  if (num_events > 8) num_events = 8;
+  for (int i = 0; i < num_events; ++i) g_prof.events[i] = events[i];
+  g_prof.num_events = num_events;
+  return KVH_OK;
+}
+
+int kvh_last_launch_kernels(int32_t* kinds, int32_t cap) {
+  const int n = g_prof.last_count;
+  for (int i = 0; i < n && i < cap && i < 8; ++i) kinds[i] = g_prof.last_kinds[i];
+  return n;
+}
+
+}  // extern "C"

@@ -1,0 +1,79 @@
+// Device-side building blocks shared by the gfx950 paged-attention kernels.
+//
+// MFMA used throughout: v_mfma_f32_16x16x32_{bf16,f16} (CDNA4). Per lane l of a wave64,
+// with j = l / 16 and n = l % 16:
+//   A operand (16 x 32): row n,    k = 8j .. 8j+7   (8 packed 16-bit values)
+//   B operand (32 x 16): column n, k = 8j .. 8j+7
+//   C/D       (16 x 16): column n, rows 4j .. 4j+3  (4 fp32 values)
+// The order of the 32 k-slots is free as long as A and B agree; the kernels use that
+// freedom to keep every lane's global loads contiguous.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kvh {
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWave = 64;
+
+// Storage-type tags. `bits16` is the raw 16-bit encoding.
+struct BF16 {
+  static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    __bf16 a = (__bf16)lo, b = (__bf16)hi;  // round to nearest even
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
+};
+
+struct F16 {
+  static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    _Float16 a = (_Float16)lo, b = (_Float16)hi;  // round to nearest even
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t x) {
+    return (float)__builtin_bit_cast(_Float16, x);
+  }
+};
+
+// Interleave the low (SEL = 0) or high (SEL = 1) 16-bit halves of two dwords:
+// result = {half(a), half(b)} with half(a) in the low 16 bits.
+template <int SEL>
+__device__ __forceinline__ uint32_t pick_halves(uint32_t a, uint32_t b) {
+  // v_perm_b32 byte selectors: bytes 0-3 come from the second operand, 4-7 from the first.
+  return SEL == 0 ? __builtin_amdgcn_perm(b, a, 0x05040100u) : __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Cross-lane reductions over the four 16-lane groups (lanes n, n+16, n+32, n+48).
+__device__ __forceinline__ float max_over_groups(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+__device__ __forceinline__ float sum_over_groups(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+__device__ __forceinline__ int64_t clamp64(int64_t x, int64_t lo, int64_t hi) {
+  return x < lo ? lo : (x > hi ? hi : x);
+}
+
+}  // namespace kvh

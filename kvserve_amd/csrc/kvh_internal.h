@@ -1,0 +1,67 @@
+// Host/device shared launch structures of libkvhip (not part of the public C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace kvh {
+
+// Everything a paged-attention kernel reads, by value in the kernel argument segment.
+// Strides are in elements; cache strides are {block, slot, head}.
+struct PAParams {
+  const void* q;
+  int64_t q_ts, q_hs;
+  const void* kc;
+  int64_t k_sb, k_ss, k_sh;
+  const void* vc;
+  int64_t v_sb, v_ss, v_sh;
+  int64_t num_blocks;
+  void* out;
+  int64_t o_ts, o_hs;
+  const int64_t* bt;
+  int64_t bt_rs;
+  const int64_t* seq_lens;
+  const int64_t* qsl;
+  int64_t T;
+  int32_t W, B, H, Hkv, G, BS;
+  float scale;     // softmax scale as given
+  float qk_scale;  // scale * log2(e): scores are kept in the exp2 domain
+  int32_t QS;      // sequences with q_len <= QS take the split-K decode kernel
+  int32_t PS;      // tokens per split-K partition (multiple of 128)
+  int32_t P;       // partitions per sequence at most: ceil(W * BS / PS)
+  float* ws_acc;   // [T, H, P, D] unnormalised partial outputs (decode class, P > 1)
+  float* ws_ml;    // [T, H, P, 2] running max (exp2 domain) and sum of each partial
+};
+
+// Launch plan: a pure function of static shapes (graph-capture safe).
+struct Plan {
+  int32_t G, QS, NT;       // GQA group, decode-class q_len cap, 16-row tiles per decode WG
+  int32_t PS, P;           // partition tokens, partitions per sequence
+  int32_t pre_rows_per_wg; // rows of one prefill workgroup
+  bool launch_prefill;     // max_query_len > QS
+  int32_t pre_tiles;       // prefill workgroups per (seq, kv_head)
+  size_t ws_acc_bytes, ws_ml_bytes, ws_bytes;
+};
+
+Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t W, int32_t BS,
+               int32_t max_q, int32_t dtype);
+
+// Kernel launchers (return hipError_t as int). `kinds` collects launched kernel kinds.
+struct LaunchLog {
+  void* const* events = nullptr;
+  int32_t num_events = 0;
+  int32_t launched = 0;
+  int32_t kinds[8] = {0};
+  void after_launch(int kind, hipStream_t s);
+};
+
+int launch_paged_attention_mfma(const PAParams& p, const Plan& plan, int32_t D, int32_t dtype,
+                                hipStream_t s, LaunchLog& log);
+int launch_paged_attention_f32(const PAParams& p, int32_t D, int32_t max_q, hipStream_t s, LaunchLog& log);
+int launch_reshape_and_cache(const void* k, int64_t k_ts, int64_t k_hs, const void* v, int64_t v_ts,
+                             int64_t v_hs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs,
+                             const int64_t* slots, int64_t T, int64_t num_blocks, int32_t Hkv, int32_t D,
+                             int32_t BS, int32_t elem_bytes, bool vec16, hipStream_t s);
+
+}  // namespace kvh

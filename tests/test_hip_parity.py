@@ -1,0 +1,228 @@
+"""HIP paged attention vs the oracle (GPU). Calls go through the C ABI via HipAttention.
+
+Mirrors the reference's parity suite (tests/test_triton_attention.py:55-86: CASES x heads x
+dtype at D=64/BS=16, plus D=128/BS=32) and adds the five BASELINE configs at full size,
+the committed golden fixtures, the exact-fp32 path and the edge cases of the contract.
+Tolerance: max-abs <= 2e-2 for bf16/fp16 storage against the oracle on the same rounded
+inputs (stricter than the reference's atol=rtol=2e-2), 1e-4 for the fp32 path.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from kvserve_amd import HipAttention, last_launch_kernels, workloads
+from kvserve_amd.attention import AttentionMetadata
+from tests import paged_check as pc
+from tests.golden.make_golden import load_fixtures
+
+pytestmark = pytest.mark.gpu
+
+HEADS = [(32, 8), (16, 16), (32, 4)]
+DTYPES = [torch.bfloat16, torch.float16]
+
+
+@pytest.mark.parametrize("case", list(workloads.REFERENCE_CASES))
+@pytest.mark.parametrize("heads", HEADS, ids=lambda h: f"{h[0]}q{h[1]}kv")
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_reference_cases(hip_device, case, heads, dtype):
+    w = workloads.reference_case(case, *heads, head_dim=64, block_size=16, seed=0)
+    b = workloads.materialize(w, dtype, hip_device, seed=0)
+    out = pc.attend(b)
+    assert pc.written_rows_match(b)
+    ref = pc.torch_oracle_full(b)
+    err = (out.float().cpu() - ref).abs().max().item()
+    assert err <= pc.TOL_16BIT, f"{case} {heads} {dtype}: max abs err {err}"
+
+
+def test_head_dim_128_and_block_32(hip_device):
+    w = workloads.custom("d128_bs32", [1, 9, 1], [80, 40, 1000], 32, 8, 128, 32, seed=0)
+    b = workloads.materialize(w, torch.bfloat16, hip_device)
+    out = pc.attend(b)
+    err = (out.float().cpu() - pc.torch_oracle_full(b)).abs().max().item()
+    assert err <= pc.TOL_16BIT, err
+
+
+def test_golden_fixtures(hip_device):
+    for name, fx in load_fixtures().items():
+        q = torch.from_numpy(fx["q_bits"].view(np.int16)).view(torch.bfloat16).to(hip_device)
+        kc = torch.from_numpy(fx["k_bits"].view(np.int16)).view(torch.bfloat16).to(hip_device)
+        vc = torch.from_numpy(fx["v_bits"].view(np.int16)).view(torch.bfloat16).to(hip_device)
+        qsl = torch.from_numpy(fx["query_start_loc"]).to(hip_device)
+        meta = AttentionMetadata(
+            slot_mapping=torch.empty(0, dtype=torch.long, device=hip_device),
+            block_tables=torch.from_numpy(fx["block_tables"]).to(hip_device),
+            seq_lens=torch.from_numpy(fx["seq_lens"]).to(hip_device),
+            query_lens=(qsl[1:] - qsl[:-1]),
+            query_start_loc=qsl,
+            max_seq_len=int(fx["seq_lens"].max()),
+            max_query_len=int(np.diff(fx["query_start_loc"]).max()),
+        )
+        out = HipAttention.forward(q, kc, vc, meta, float(fx["scale"]))
+        err = np.abs(out.double().cpu().numpy() - fx["out"]).max()
+        assert err <= pc.TOL_16BIT, f"{name}: {err}"
+
+
+@pytest.mark.parametrize("case", list(workloads.REFERENCE_CASES))
+def test_fp32_path(hip_device, case):
+    w = workloads.reference_case(case, 32, 8, head_dim=64, block_size=16, seed=1)
+    b = workloads.materialize(w, torch.float32, hip_device, seed=1)
+    out = pc.attend(b)
+    assert last_launch_kernels() == ["f32"]
+    err = pc.max_err_vs_oracle(b, out, list(range(len(w.query_lens))))
+    assert err <= pc.TOL_F32, err
+
+
+def test_fp32_any_block_size(hip_device):
+    """The exact-fp32 path serves the reference's CPU-only block sizes too (e.g. 4)."""
+    w = workloads.custom("bs4", [3, 1, 7], [9, 30, 0], 8, 2, 64, 4, seed=2)
+    b = workloads.materialize(w, torch.float32, hip_device, seed=2)
+    out = pc.attend(b)
+    assert pc.max_err_vs_oracle(b, out, [0, 1, 2]) <= pc.TOL_F32
+
+
+@pytest.mark.parametrize("idx", [1, 2, 3, 4, 5])
+def test_baseline_configs(hip_device, idx):
+    """BASELINE configs at full size: write + attend, then the fp64 oracle on sampled
+    sequences/rows, plus size-independent properties (finite output, written rows exact)."""
+    w = workloads.baseline_config(idx, seed=0)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=idx)
+    out = pc.attend(b)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert pc.written_rows_match(b)
+    nseq = len(w.query_lens)
+    if idx == 3:  # 512 decodes then 4 prefills: sample decodes, all prefills at 24 rows
+        seqs = list(range(0, 512, 16)) + [511, 512, 513, 514, 515]
+        err = pc.max_err_vs_oracle(b, out, seqs, rows_per_seq=24)
+    else:
+        seqs = list(range(nseq)) if nseq <= 64 else list(range(0, nseq, 4))
+        err = pc.max_err_vs_oracle(b, out, seqs)
+    print(f"config {idx}: max abs err vs fp64 oracle {err:.3e}; kernels {last_launch_kernels()}")
+    assert err <= pc.TOL_16BIT, err
+
+
+def test_out_argument_and_strided_inputs(hip_device):
+    """out= a slice of a larger static buffer (piecewise mode, cuda_graph.py:240); q and v
+    strided views of a fused QKV output (model.py:89-92)."""
+    H, Hkv, D = 32, 8, 128
+    w = workloads.custom("strided", [1, 5, 1, 30], [100, 60, 7, 0], H, Hkv, D, 16, seed=3)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=3)
+    T = w.num_tokens
+    qkv = torch.randn(T, (H + 2 * Hkv) * D, device=hip_device, dtype=torch.bfloat16)
+    q, k, v = qkv.split([H * D, Hkv * D, Hkv * D], dim=-1)
+    q, k, v = q.view(T, H, D), k.view(T, Hkv, D), v.view(T, Hkv, D)
+    assert not q.is_contiguous() and not v.is_contiguous()
+    kc2, vc2 = b.k_cache.clone(), b.v_cache.clone()
+    HipAttention.write_kv(b.k_cache, b.v_cache, k, v, b.meta.slot_mapping)
+    HipAttention.write_kv(kc2, vc2, k.contiguous(), v.contiguous(), b.meta.slot_mapping)
+    assert torch.equal(b.k_cache.view(torch.int16), kc2.view(torch.int16))
+    assert torch.equal(b.v_cache.view(torch.int16), vc2.view(torch.int16))
+    static = torch.full((T + 7, H, D), float("nan"), device=hip_device, dtype=torch.bfloat16)
+    dst = static[:T]
+    ret = HipAttention.forward(q, b.k_cache, b.v_cache, b.meta, w.scale, out=dst)
+    assert ret is dst
+    ref = HipAttention.forward(q.contiguous(), b.k_cache, b.v_cache, b.meta, w.scale)
+    assert torch.equal(dst.view(torch.int16), ref.view(torch.int16))
+    assert torch.isnan(static[T:].float()).all()  # nothing written past the real rows
+    b.q = q
+    assert pc.max_err_vs_oracle(b, dst, [0, 1, 2, 3]) <= pc.TOL_16BIT
+
+
+def test_stale_slots_and_columns_never_read(hip_device):
+    """Slots past seq_len hold NaN, and table columns past ceil(seq_len / BS) point at
+    all-NaN blocks (stale graph rows, cuda_graph.py:129-134): the output stays exact."""
+    H, Hkv, D, BS = 32, 8, 128, 16
+    w = workloads.custom("stale", [1, 1, 3, 1], [40, 511, 77, 4000], H, Hkv, D, BS, seed=4, spare_blocks=16)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=4)
+    used = set()
+    for t, s in zip(w.tables, w.seq_lens):
+        nblk = -(-s // BS)
+        used.update(t[:nblk])
+        last = t[nblk - 1]
+        tail = s - (nblk - 1) * BS
+        b.k_cache[last, tail:] = float("nan")
+        b.v_cache[last, tail:] = float("nan")
+    spare = [i for i in range(w.num_blocks) if i not in used]
+    b.k_cache[spare] = float("nan")
+    b.v_cache[spare] = float("nan")
+    width = w.table_width() + 64
+    bt = torch.tensor(spare[:1], device=hip_device).repeat(len(w.tables), width)
+    for i, t in enumerate(w.tables):
+        bt[i, : len(t)] = torch.tensor(t)
+    b.meta.block_tables = bt
+    out = pc.attend(b)
+    assert torch.isfinite(out.float()).all()
+    assert pc.max_err_vs_oracle(b, out, [0, 1, 2, 3]) <= pc.TOL_16BIT
+
+
+def test_split_k_matches_single_pass(hip_device):
+    """The same batch with a wide table (split-K partitions + log-sum-exp reduce) and a
+    narrow one (one partition per sequence) agree within accumulation rounding."""
+    w = workloads.custom("split", [1] * 8, [4000, 17, 900, 2047, 3, 1500, 64, 3999], 32, 8, 128, 16, seed=5)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=5)
+    HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping)
+    narrow = HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale)
+    k_narrow = last_launch_kernels()
+    bt = torch.zeros(8, 8192, dtype=torch.long, device=hip_device)
+    bt[:, : b.meta.block_tables.shape[1]] = b.meta.block_tables
+    b.meta.block_tables = bt
+    wide = HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale)
+    k_wide = last_launch_kernels()
+    assert "reduce" in k_wide, k_wide
+    assert (narrow.float() - wide.float()).abs().max().item() <= 1e-2
+    assert pc.max_err_vs_oracle(b, wide, list(range(8))) <= pc.TOL_16BIT
+    print("narrow:", k_narrow, "wide:", k_wide)
+
+
+def test_mixed_batch_dispatch(hip_device):
+    """Decode-class rows take the split-K kernel and longer queries the prefill kernel,
+    both launched over the same metadata with no host synchronisation."""
+    w = workloads.reference_case("mixed", 32, 8, head_dim=128, block_size=16)
+    b = workloads.materialize(w, torch.bfloat16, hip_device)
+    out = pc.attend(b)
+    kinds = last_launch_kernels()
+    assert kinds[0] == "decode" and "prefill" in kinds, kinds
+    assert pc.max_err_vs_oracle(b, out, list(range(5))) <= pc.TOL_16BIT
+    dec = workloads.reference_case("decode", 32, 8, head_dim=128, block_size=16)
+    bd = workloads.materialize(dec, torch.bfloat16, hip_device)
+    pc.attend(bd)
+    assert "prefill" not in last_launch_kernels()
+
+
+def test_rows_without_keys_write_zeros(hip_device):
+    """seq_len < q_len leaves early rows with no visible key: they come out as zeros (the
+    reference divides by l = 0 -> 1, kernels/paged_attention.py:113)."""
+    w = workloads.custom("nokeys", [4], [0], 32, 8, 128, 16, seed=6)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=6)
+    b.meta.seq_lens = torch.tensor([2], dtype=torch.long, device=hip_device)  # ctx = -2
+    out = HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale)
+    assert torch.count_nonzero(out[:2].float()) == 0
+    assert torch.isfinite(out.float()).all()
+
+
+def test_empty_batch(hip_device):
+    q = torch.empty(0, 32, 128, device=hip_device, dtype=torch.bfloat16)
+    kc = torch.zeros(4, 16, 8, 128, device=hip_device, dtype=torch.bfloat16)
+    meta = AttentionMetadata(
+        slot_mapping=torch.empty(0, dtype=torch.long, device=hip_device),
+        block_tables=torch.zeros(0, 1, dtype=torch.long, device=hip_device),
+        seq_lens=torch.zeros(0, dtype=torch.long, device=hip_device),
+        query_lens=torch.zeros(0, dtype=torch.long, device=hip_device),
+        query_start_loc=torch.zeros(1, dtype=torch.long, device=hip_device),
+        max_seq_len=0,
+        max_query_len=0,
+    )
+    out = HipAttention.forward(q, kc, kc, meta, 0.1)
+    assert out.shape == (0, 32, 128)
+    HipAttention.write_kv(kc, kc, q[:, :8], q[:, :8], meta.slot_mapping)
+
+
+def test_argument_errors_raise(hip_device):
+    w = workloads.reference_case("decode", 32, 8, head_dim=128)
+    b = workloads.materialize(w, torch.bfloat16, hip_device)
+    with pytest.raises(ValueError):
+        HipAttention.forward(b.q.float(), b.k_cache, b.v_cache, b.meta, w.scale)
+    bad = torch.empty(b.k_cache.shape[:3] + (96,), dtype=torch.bfloat16, device=hip_device)
+    with pytest.raises((ValueError, RuntimeError)):
+        HipAttention.forward(b.q[..., :96].contiguous(), bad, bad, b.meta, w.scale)

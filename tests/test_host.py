@@ -1,0 +1,206 @@
+"""Host-side checks that need no GPU: the C ABI library, the plan, the Python boundary."""
+
+import ctypes
+import math
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from kvserve_amd import _lib, attention, workloads
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "kvhip.h"
+
+E_NULL, E_SHAPE, E_DTYPE, E_ALIGN, E_UNSUPPORTED, E_WORKSPACE = -1, -2, -3, -4, -5, -6
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    return re.findall(r"KVH_API\s+[\w\s\*]+?\b(kvh_\w+)\s*\(", text)
+
+
+def test_header_declares_the_abi():
+    names = declared_symbols()
+    assert set(names) == set(_lib.SIGNATURES), names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.kvh_abi_version() == _lib.ABI_VERSION
+
+
+def test_strerror_covers_every_status(lib):
+    for code in (0, E_NULL, E_SHAPE, E_DTYPE, E_ALIGN, E_UNSUPPORTED, E_WORKSPACE):
+        msg = lib.kvh_strerror(code).decode()
+        assert msg and (code == 0 or "kvhip" in msg)
+    assert lib.kvh_strerror(-99).decode() == "kvhip: unknown status"
+
+
+def _attn_args(**over):
+    """Arguments of kvh_paged_attention for a C2-like shape with fake (never dereferenced)
+    16-byte-aligned pointers; every call below fails validation before any HIP call."""
+    a = dict(
+        q=0x1000, q_ts=32 * 128, q_hs=128, kc=0x2000, kcs=(16 * 8 * 128, 8 * 128, 128), vc=0x3000,
+        vcs=(16 * 8 * 128, 8 * 128, 128), nb=40_000, out=0x4000, o_ts=32 * 128, o_hs=128, bt=0x5000,
+        bt_rs=512, W=512, sl=0x6000, qsl=0x7000, T=64, B=64, H=32, Hkv=8, D=128, BS=16, max_q=1,
+        scale=128**-0.5, dtype=2, ws=0, ws_bytes=0, stream=None,
+    )  # fmt: skip
+    a.update(over)
+    return a
+
+
+def _call(lib, a):
+    return lib.kvh_paged_attention(
+        a["q"], a["q_ts"], a["q_hs"], a["kc"], _lib.i64x3(a["kcs"]), a["vc"], _lib.i64x3(a["vcs"]), a["nb"],
+        a["out"], a["o_ts"], a["o_hs"], a["bt"], a["bt_rs"], a["W"], a["sl"], a["qsl"], a["T"], a["B"], a["H"],
+        a["Hkv"], a["D"], a["BS"], a["max_q"], a["scale"], a["dtype"], a["ws"], a["ws_bytes"], a["stream"],
+    )  # fmt: skip
+
+
+@pytest.mark.parametrize(
+    ("over", "status"),
+    [
+        (dict(dtype=7), E_DTYPE),
+        (dict(H=30), E_SHAPE),
+        (dict(D=96), E_UNSUPPORTED),
+        (dict(BS=8), E_UNSUPPORTED),
+        (dict(Hkv=0), E_SHAPE),
+        (dict(W=0), E_SHAPE),
+        (dict(q=0), E_NULL),
+        (dict(bt_rs=100), E_SHAPE),
+        (dict(q=0x1008), E_ALIGN),
+        (dict(q_hs=132), E_ALIGN),
+        (dict(ws=0, ws_bytes=0), E_WORKSPACE),  # C2 needs split-K scratch
+        (dict(dtype=0, D=102), E_UNSUPPORTED),
+        (dict(B=70_000), E_UNSUPPORTED),
+    ],
+)
+def test_attention_validation(lib, over, status):
+    assert _call(lib, _attn_args(**over)) == status
+
+
+def test_empty_batch_is_a_no_op(lib):
+    assert _call(lib, _attn_args(T=0, q=0, out=0)) == 0
+    assert _call(lib, _attn_args(B=0)) == 0
+
+
+def test_cache_write_validation(lib):
+    f = lib.kvh_reshape_and_cache
+    strides = _lib.i64x3((16 * 8 * 128, 8 * 128, 128))
+    args = [0x1000, 8 * 128, 128, 0x2000, 8 * 128, 128, 0x3000, strides, 0x4000, strides, 0x5000, 10, 100, 8, 128, 16]
+    assert f(*args, 9, None) == E_DTYPE
+    assert f(*args[:11], 0, *args[12:], 2, None) == 0  # no tokens: nothing to launch
+    bad = list(args)
+    bad[0] = 0
+    assert f(*bad, 2, None) == E_NULL
+    bad = list(args)
+    bad[0] = 0x1001
+    assert f(*bad, 2, None) == E_ALIGN
+
+
+def test_workspace_follows_the_plan(lib):
+    ws = lib.kvh_paged_attention_workspace_size
+    # W = 8 -> 128 keys: a single partition, no workspace
+    assert ws(8, 8, 32, 8, 64, 8, 16, 1, 2) == 0
+    # C1: 8 seqs x 8 kv heads is a small grid, so 512 keys split into 4 partitions of 128
+    want = math.ceil(8 * 32 * 4 * 64 * 4 / 256) * 256 + math.ceil(8 * 32 * 4 * 2 * 4 / 256) * 256
+    assert ws(8, 8, 32, 8, 64, 32, 16, 1, 2) == want
+    # C2: 64 x 8, W = 512 -> partitions of 512 tokens, 16 per sequence
+    P = 16
+    want = math.ceil(64 * 32 * P * 128 * 4 / 256) * 256 + math.ceil(64 * 32 * P * 2 * 4 / 256) * 256
+    assert ws(64, 64, 32, 8, 128, 512, 16, 1, 2) == want
+    assert ws(64, 64, 32, 8, 128, 512, 16, 1, 0) == 0  # fp32 path: no split
+    assert ws(64, 64, 30, 8, 128, 512, 16, 1, 2) == 0  # invalid shape
+
+
+def test_get_backend_contract(monkeypatch):
+    with pytest.raises(ValueError):
+        attention.get_backend("torch", "cuda", 16)
+    with pytest.raises(ValueError):
+        attention.get_backend("nope", "cuda", 16)
+    if not attention.hip_available():
+        with pytest.raises(RuntimeError):
+            attention.get_backend("hip", "cuda", 16)
+        with pytest.raises(RuntimeError):
+            attention.get_backend("auto", "cpu", 16)
+    monkeypatch.setattr(attention, "hip_available", lambda: True)
+    assert attention.get_backend("hip", "cuda", 16) is attention.HipAttention
+    assert attention.get_backend("auto", "cuda", 32) is attention.HipAttention
+    with pytest.raises(ValueError):
+        attention.get_backend("hip", "cuda", 8)
+    cls = attention.HipAttention
+    assert cls.graph_capturable and not cls.needs_padded_layout
+
+
+def test_build_metadata_layout():
+    tables = [[5, 2], [7], [1, 3, 4]]
+    m = attention.build_metadata("cpu", tables, [81, 112, 50, 51], [20, 1, 40], [2, 1, 1], padded_layout=True)
+    assert m.block_tables.tolist() == [[5, 2, 0], [7, 0, 0], [1, 3, 4]]  # 0-padded
+    assert m.query_start_loc.tolist() == [0, 2, 3, 4]
+    assert m.max_seq_len == 40 and m.max_query_len == 2
+    for t in (m.slot_mapping, m.block_tables, m.seq_lens, m.query_lens, m.query_start_loc):
+        assert t.dtype == torch.int64
+    assert m.q_gather.tolist() == [[0, 1], [2, 0], [3, 0]]
+    assert m.q_valid.tolist() == [[True, True], [True, False], [True, False]]
+    assert attention.build_metadata("cpu", tables, [1, 2, 3, 4], [20, 1, 40], [2, 1, 1]).q_gather is None
+
+
+def test_baseline_config_shapes():
+    c1, c2, c3, c4, c5 = (workloads.baseline_config(i) for i in range(1, 6))
+    assert (len(c1.seq_lens), c1.num_heads, c1.num_kv_heads, c1.head_dim) == (8, 32, 8, 64)
+    assert all(64 <= s <= 512 for s in c1.seq_lens) and c1.num_blocks == 512
+    assert (len(c2.seq_lens), c2.head_dim) == (64, 128) and all(1024 <= s <= 8192 for s in c2.seq_lens)
+    assert c3.num_tokens == 2048 and c3.query_lens.count(384) == 4 and c3.query_lens.count(1) == 512
+    assert all(0 <= c <= 4096 for c in c3.context_lens[512:])
+    assert all(256 <= s <= 4096 for s in c3.seq_lens[:512])
+    assert all(t[:750] == c4.tables[0][:750] for t in c4.tables)
+    assert all(16_000 <= s <= 32_000 for s in c4.seq_lens) and c4.table_width() == 2000
+    assert c5.query_lens == [5] * 32 and all(2048 <= c <= 4096 for c in c5.context_lens)
+    for w in (c1, c2, c3, c5):  # disjoint physical blocks
+        used = [b for t in w.tables for b in t]
+        assert len(used) == len(set(used)) and max(used) < w.num_blocks
+
+
+def test_byte_and_flop_formulas():
+    w = workloads.custom("tiny", [1, 3], [20, 4], 4, 2, 64, 16)
+    # seq_lens 21 and 7; keys bytes = 2 * Hkv * D * e * tokens
+    assert w.kv_bytes(2) == 2 * 2 * 64 * 2 * 28
+    assert w.algorithmic_bytes(2) == w.kv_bytes(2) + 2 * 4 * 4 * 64 * 2 + 8 * (2 + 1) + 8 * 7
+    # visible (row, key) pairs: 21 + (5 + 6 + 7) = 39
+    assert w.flops() == 4 * 4 * 64 * 39
+    c4 = workloads.baseline_config(4)
+    shared = 750 * 16
+    assert c4.unique_tokens() == shared + sum(s - shared for s in c4.seq_lens)
+
+
+def test_product_never_imports_the_oracle():
+    pkg = ROOT / "kvserve_amd"
+    for f in list(pkg.rglob("*.py")) + list(pkg.rglob("*.hip")) + list(pkg.rglob("*.h")):
+        text = f.read_text()
+        assert not re.search(r"^\s*(from|import)\s+oracle\b", text, re.M), f
+        assert "liboracle" not in text, f
+
+
+def test_load_fails_loudly_without_library(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libkvhip.so")
+    with pytest.raises(RuntimeError, match="no fallback"):
+        _lib.load()
+
+
+def test_ctypes_signatures_match_header():
+    text = HEADER.read_text()
+    for name, (_, args) in _lib.SIGNATURES.items():
+        m = re.search(r"KVH_API[^;(]*?\b" + name + r"\s*\(([^;]*?)\)\s*;", text, re.S)
+        assert m, name
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(args), (name, len(params), len(args))
+    assert ctypes.sizeof(ctypes.c_size_t) == 8
