@@ -161,28 +161,31 @@ def cpu_baseline(idx: int, budget_s: float, seed: int = 0) -> dict:
     torch.set_num_threads(threads)
     w = workloads.baseline_config(idx, seed=seed)
     b = workloads.materialize(w, torch.bfloat16, "cuda:0", seed=seed)
-    done_bytes, spent, n = 0, 0.0, 0
+    # stage the sample on the host once: the timed region is the CPU attention only
+    seqs = []
     for s in range(len(w.seq_lens)):
         table = torch.tensor(w.tables[s], device="cuda:0")
-        kc = b.k_cache.index_select(0, table).float().cpu()
-        vc = b.v_cache.index_select(0, table).float().cpu()
         q0 = sum(w.query_lens[:s])
-        q = b.q[q0 : q0 + w.query_lens[s]].float().cpu()
-        bt = torch.arange(len(w.tables[s]), dtype=torch.long)[None]
-        sl = torch.tensor([w.seq_lens[s]])
-        ql = torch.tensor([w.query_lens[s]])
-        t0 = time.perf_counter()
-        torch_reference.forward(q, kc, vc, bt, sl, ql, w.scale)
-        dt = time.perf_counter() - t0
-        if s == 0:
-            continue  # warm-up sequence, not counted
-        sub = workloads.Workload("s", [w.query_lens[s]], [w.seq_lens[s]], [w.tables[s]], w.num_blocks, w.num_heads,
-                                 w.num_kv_heads, w.head_dim, w.block_size)  # fmt: skip
-        done_bytes += sub.algorithmic_bytes(2)
-        spent += dt
-        n += 1
-        if spent >= budget_s:
-            break
+        seqs.append((
+            b.q[q0 : q0 + w.query_lens[s]].float().cpu(),
+            b.k_cache.index_select(0, table).float().cpu(),
+            b.v_cache.index_select(0, table).float().cpu(),
+            torch.arange(len(w.tables[s]), dtype=torch.long)[None],
+            torch.tensor([w.seq_lens[s]]),
+            torch.tensor([w.query_lens[s]]),
+            workloads.Workload("s", [w.query_lens[s]], [w.seq_lens[s]], [w.tables[s]], w.num_blocks, w.num_heads,
+                               w.num_kv_heads, w.head_dim, w.block_size).algorithmic_bytes(2),
+        ))  # fmt: skip
+    torch_reference.forward(*seqs[0][:6], w.scale)  # warm-up, untimed
+    done_bytes, spent, n, passes = 0, 0.0, 0, 0
+    while spent < budget_s and passes < 50:
+        passes += 1
+        for q, kc, vc, bt, sl, ql, nbytes in seqs:
+            t0 = time.perf_counter()
+            torch_reference.forward(q, kc, vc, bt, sl, ql, w.scale)
+            spent += time.perf_counter() - t0
+            done_bytes += nbytes
+            n += 1
     del b
     torch.cuda.empty_cache()
     cpu = platform.processor() or platform.machine()
@@ -198,8 +201,8 @@ def cpu_baseline(idx: int, budget_s: float, seed: int = 0) -> dict:
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n} of {len(w.seq_lens)} sequences of {w.name} (first one untimed), fp32 torch "
-        f"gather+repeat_interleave+masked SDPA, one sequence per call, {spent:.1f} s timed",
+        "sample": f"{passes} pass(es) over the {len(w.seq_lens)} sequences of {w.name} ({n} calls, one sequence "
+        f"per call), fp32 torch gather+repeat_interleave+masked SDPA, {spent:.1f} s timed",
         "cpu_model": cpu,
         "ms_per_seq": 1e3 * spent / max(n, 1),
     }
