@@ -38,6 +38,10 @@ HIP_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA sources/results in ordinary VGPRs: the softmax rescale touches the accumulators
+    # every chunk, and AGPR copies would cost two moves per accumulator register.
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
 ]
 
 
@@ -58,15 +62,22 @@ def _run(cmd: list[str]) -> None:
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
-    """Compile all sources (always; no staleness check) and link the shared library."""
-    BUILD.mkdir(exist_ok=True)
-    LIB_DIR.mkdir(exist_ok=True)
+def build(
+    verbose: bool = False, extra_flags: list[str] | None = None, out: Path | None = None, build_dir: Path | None = None
+) -> Path:
+    """Compile all sources (always; no staleness check) and link the shared library.
+
+    `extra_flags` (e.g. -D tuning macros), `out` and `build_dir` let a tuning sweep build
+    variants next to the default kvserve_amd/lib/libkvhip.so."""
+    lib = Path(out) if out else LIB
+    objdir = Path(build_dir) if build_dir else BUILD
+    objdir.mkdir(parents=True, exist_ok=True)
+    lib.parent.mkdir(parents=True, exist_ok=True)
     cc = hipcc()
     flags = HIP_FLAGS + list(extra_flags or [])
 
     def compile_one(src: str) -> Path:
-        obj = BUILD / (Path(src).stem + ".o")
+        obj = objdir / (Path(src).stem + ".o")
         cmd = [cc, *flags, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd))
@@ -76,13 +87,13 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
     jobs = min(len(SOURCES), int(os.environ.get("MAX_JOBS", "8")), 16)
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         objs = list(ex.map(compile_one, SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [cc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     if verbose:
         print(" ".join(cmd))
     _run(cmd)
-    os.replace(tmp, LIB)  # atomic: a process that already mapped the old file keeps it
-    return LIB
+    os.replace(tmp, lib)  # atomic: a process that already mapped the old file keeps it
+    return lib
 
 
 if __name__ == "__main__":

@@ -3,7 +3,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-#include "../../include/kvhip.h"
+#include "kvhip.h"  // include/ is on the include path
 #include "kvh_device.h"
 #include "kvh_internal.h"
 
@@ -27,17 +27,6 @@ struct ProfileState {
 };
 thread_local ProfileState g_prof;
 
-// Tokens per split-K partition; KVH_PARTITION_TOKENS (a multiple of 128) overrides the
-// heuristic, for tuning sweeps.
-int partition_override() {
-  static int v = [] {
-    const char* s = getenv("KVH_PARTITION_TOKENS");
-    int x = s ? atoi(s) : 0;
-    return (x >= 128 && x % 128 == 0) ? x : 0;
-  }();
-  return v;
-}
-
 }  // namespace
 
 void LaunchLog::after_launch(int kind, hipStream_t s) {
@@ -48,41 +37,37 @@ void LaunchLog::after_launch(int kind, hipStream_t s) {
 
 Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t W, int32_t BS, int32_t max_q,
                int32_t dtype) {
+  (void)W;
+  (void)BS;
   Plan pl{};
   pl.G = H / Hkv;
   if (max_q < 1) max_q = 1;
   const int G = pl.G;
   if ((int64_t)max_q * G <= 64) {
-    // decode / speculative-verify batch: every sequence takes the split-K kernel
+    // decode / speculative-verify batch: every sequence takes the stream-K decode kernel
     pl.QS = max_q;
     pl.launch_prefill = false;
   } else {
-    // mixed batch: single-tile rows split-K, everything longer on the prefill kernel
+    // mixed batch: single-tile rows stream-K, everything longer on the prefill kernel
     pl.QS = G >= 16 ? 1 : 16 / G;
     pl.launch_prefill = true;
   }
   pl.NT = (pl.QS * G + 15) / 16;
+  pl.RS = pl.QS * G;
+  pl.HGW = Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1);
   pl.pre_rows_per_wg = 128;
   pl.pre_tiles = (int32_t)(((int64_t)max_q * G + pl.pre_rows_per_wg - 1) / pl.pre_rows_per_wg);
-  const int64_t max_keys = (int64_t)W * BS;
-  int ps = partition_override();
-  if (!ps) {
-    // Smallest partition (>= 128 tokens = one 32-token chunk per wave) that keeps the grid
-    // near 8K workgroups: enough to fill 256 CUs several times over while keeping the
-    // partial-result traffic a few percent of the KV bytes.
-    ps = 128;
-    while (ps < max_keys && (int64_t)B * Hkv * ((max_keys + ps - 1) / ps) > 8192) ps *= 2;
-  }
-  pl.PS = ps;
-  pl.P = (int32_t)((max_keys + ps - 1) / ps);
-  if (pl.P < 1) pl.P = 1;
-  if (dtype == KVH_DTYPE_F32 || pl.P == 1) {
-    pl.ws_acc_bytes = pl.ws_ml_bytes = pl.ws_bytes = 0;
+  pl.slots = (int64_t)B * Hkv / pl.HGW + kMaxDecodeWaves / pl.HGW;
+  if (dtype == KVH_DTYPE_F32) {
+    pl.ws_acc_bytes = pl.ws_ml_bytes = pl.ws_cum_bytes = pl.ws_bytes = 0;
   } else {
-    pl.ws_acc_bytes = align_up((size_t)T * H * pl.P * D * sizeof(float));
-    pl.ws_ml_bytes = align_up((size_t)T * H * pl.P * 2 * sizeof(float));
-    pl.ws_bytes = pl.ws_acc_bytes + pl.ws_ml_bytes;
+    const size_t rows = (size_t)pl.slots * pl.HGW * pl.RS;
+    pl.ws_acc_bytes = align_up(rows * D * sizeof(float));
+    pl.ws_ml_bytes = align_up(rows * 2 * sizeof(float));
+    pl.ws_cum_bytes = align_up(((size_t)B + 1) * sizeof(int32_t));
+    pl.ws_bytes = pl.ws_acc_bytes + pl.ws_ml_bytes + pl.ws_cum_bytes;
   }
+  (void)T;
   return pl;
 }
 
@@ -191,7 +176,8 @@ int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stri
   if (!q || !k_cache || !v_cache || !k_cache_strides || !v_cache_strides || !out || !block_tables || !seq_lens ||
       !query_start_loc)
     return KVH_E_NULL;
-  if (num_blocks < 0 || bt_row_stride < max_blocks_per_seq) return KVH_E_SHAPE;
+  // num_blocks >= 1: the kernels read block 0 in place of an absent tile (and mask it out)
+  if (num_blocks < 1 || bt_row_stride < max_blocks_per_seq) return KVH_E_SHAPE;
   const int64_t strides[] = {q_tok_stride, q_head_stride, o_tok_stride, o_head_stride,
                              k_cache_strides[0], k_cache_strides[1], k_cache_strides[2],
                              v_cache_strides[0], v_cache_strides[1], v_cache_strides[2]};
@@ -237,10 +223,12 @@ int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stri
   p.scale = scale;
   p.qk_scale = scale * kLog2e;
   p.QS = plan.QS;
-  p.PS = plan.PS;
-  p.P = plan.P;
+  p.RS = plan.RS;
+  p.HGW = plan.HGW;
+  p.NU = 0;  // set by the decode launcher from the device's occupancy
   p.ws_acc = plan.ws_bytes ? (float*)workspace : nullptr;
   p.ws_ml = plan.ws_bytes ? (float*)((char*)workspace + plan.ws_acc_bytes) : nullptr;
+  p.ws_cum = plan.ws_bytes ? (int32_t*)((char*)workspace + plan.ws_acc_bytes + plan.ws_ml_bytes) : nullptr;
 
   hipStream_t s = (hipStream_t)stream;
   if (n_armed > 0) {

@@ -7,6 +7,10 @@
 
 namespace kvh {
 
+// Upper bound on the waves one decode launch uses (256 CUs x 8 waves per SIMD x 4 SIMDs
+// would be 8192); the workspace is sized for it, so its size never depends on the device.
+constexpr int32_t kMaxDecodeWaves = 8192;
+
 // Everything a paged-attention kernel reads, by value in the kernel argument segment.
 // Strides are in elements; cache strides are {block, slot, head}.
 struct PAParams {
@@ -27,25 +31,28 @@ struct PAParams {
   int32_t W, B, H, Hkv, G, BS;
   float scale;     // softmax scale as given
   float qk_scale;  // scale * log2(e): scores are kept in the exp2 domain
-  int32_t QS;      // sequences with q_len <= QS take the split-K decode kernel
-  int32_t PS;      // tokens per split-K partition (multiple of 128)
-  int32_t P;       // partitions per sequence at most: ceil(W * BS / PS)
-  float* ws_acc;   // [T, H, P, D] unnormalised partial outputs (decode class, P > 1)
-  float* ws_ml;    // [T, H, P, 2] running max (exp2 domain) and sum of each partial
+  int32_t QS;      // sequences with 0 < q_len <= QS are decode class (stream-K kernel)
+  int32_t RS;      // query rows of a decode-class sequence at most: QS * G
+  int32_t HGW;     // kv heads (waves) per work unit of the decode kernel: 4, 2 or 1
+  int32_t NU;      // work units the decode launch provides (waves / HGW)
+  float* ws_acc;   // [slots, HGW, RS, D] unnormalised partial outputs of split segments
+  float* ws_ml;    // [slots, HGW, RS, 2] running max (exp2 domain) and sum of each partial
+  int32_t* ws_cum; // [B + 1] prefix sums of decode chunks per kv head, written by the decode kernel
 };
 
 // Launch plan: a pure function of static shapes (graph-capture safe).
 struct Plan {
-  int32_t G, QS, NT;       // GQA group, decode-class q_len cap, 16-row tiles per decode WG
-  int32_t PS, P;           // partition tokens, partitions per sequence
-  int32_t pre_rows_per_wg; // rows of one prefill workgroup
-  bool launch_prefill;     // max_query_len > QS
-  int32_t pre_tiles;       // prefill workgroups per (seq, kv_head)
-  size_t ws_acc_bytes, ws_ml_bytes, ws_bytes;
+  int32_t G, QS, NT, RS;    // GQA group, decode-class q_len cap, 16-row tiles, rows per sequence
+  int32_t HGW;              // kv heads per decode work unit
+  int32_t pre_rows_per_wg;  // rows of one prefill workgroup
+  bool launch_prefill;      // max_query_len > QS
+  int32_t pre_tiles;        // prefill workgroups per (seq, kv_head)
+  int64_t slots;            // partial slots: B * Hkv / HGW + kMaxDecodeWaves / HGW
+  size_t ws_acc_bytes, ws_ml_bytes, ws_cum_bytes, ws_bytes;
 };
 
-Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t W, int32_t BS,
-               int32_t max_q, int32_t dtype);
+Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t W, int32_t BS, int32_t max_q,
+               int32_t dtype);
 
 // Kernel launchers (return hipError_t as int). `kinds` collects launched kernel kinds.
 struct LaunchLog {
@@ -56,8 +63,8 @@ struct LaunchLog {
   void after_launch(int kind, hipStream_t s);
 };
 
-int launch_paged_attention_mfma(const PAParams& p, const Plan& plan, int32_t D, int32_t dtype,
-                                hipStream_t s, LaunchLog& log);
+int launch_paged_attention_mfma(PAParams& p, const Plan& plan, int32_t D, int32_t dtype, hipStream_t s,
+                                LaunchLog& log);
 int launch_paged_attention_f32(const PAParams& p, int32_t D, int32_t max_q, hipStream_t s, LaunchLog& log);
 int launch_reshape_and_cache(const void* k, int64_t k_ts, int64_t k_hs, const void* v, int64_t v_ts,
                              int64_t v_hs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs,

@@ -107,16 +107,21 @@ def test_cache_write_validation(lib):
 
 
 def test_workspace_follows_the_plan(lib):
+    """Partial slots: one per (sequence, head group) plus one per possible decode work unit
+    (8192 waves / 4 heads per unit), each holding RS = QS * G rows; plus the chunk prefix sums."""
     ws = lib.kvh_paged_attention_workspace_size
-    # W = 8 -> 128 keys: a single partition, no workspace
-    assert ws(8, 8, 32, 8, 64, 8, 16, 1, 2) == 0
-    # C1: 8 seqs x 8 kv heads is a small grid, so 512 keys split into 4 partitions of 128
-    want = math.ceil(8 * 32 * 4 * 64 * 4 / 256) * 256 + math.ceil(8 * 32 * 4 * 2 * 4 / 256) * 256
-    assert ws(8, 8, 32, 8, 64, 32, 16, 1, 2) == want
-    # C2: 64 x 8, W = 512 -> partitions of 512 tokens, 16 per sequence
-    P = 16
-    want = math.ceil(64 * 32 * P * 128 * 4 / 256) * 256 + math.ceil(64 * 32 * P * 2 * 4 / 256) * 256
-    assert ws(64, 64, 32, 8, 128, 512, 16, 1, 2) == want
+
+    def want(B, Hkv, G, QS, D, hgw=4):
+        slots = B * Hkv // hgw + 8192 // hgw
+        rows = slots * hgw * QS * G
+        up = lambda x: -(-x // 256) * 256  # noqa: E731
+        return up(rows * D * 4) + up(rows * 2 * 4) + up((B + 1) * 4)
+
+    assert ws(8, 8, 32, 8, 64, 32, 16, 1, 2) == want(8, 8, 4, 1, 64)  # C1
+    assert ws(64, 64, 32, 8, 128, 512, 16, 1, 2) == want(64, 8, 4, 1, 128)  # C2
+    assert ws(160, 32, 32, 8, 128, 257, 16, 5, 2) == want(32, 8, 4, 5, 128)  # C5: verify rows
+    assert ws(2048, 516, 32, 8, 128, 280, 16, 384, 2) == want(516, 8, 4, 4, 128)  # C3: QS = 16 / G
+    assert ws(8, 8, 16, 2, 64, 32, 16, 1, 2) == want(8, 2, 8, 1, 64, hgw=2)  # two kv heads
     assert ws(64, 64, 32, 8, 128, 512, 16, 1, 0) == 0  # fp32 path: no split
     assert ws(64, 64, 30, 8, 128, 512, 16, 1, 2) == 0  # invalid shape
 
