@@ -16,7 +16,9 @@ block-table/length metadata + the cache write's read and write. The 1.2 GB worki
 Also printed in the same JSON line:
   roofline     - the decode kernel's algorithmic bytes / its mean launch duration, from HIP
                  events the library records around each of its kernels (kvh_profile_arm), vs
-                 the 8 TB/s HBM peak;
+                 the 8 TB/s HBM peak; `traffic` is the kernel's HBM bytes per launch from two
+                 child rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) calibrated on a plain
+                 copy of known size;
   cpu_baseline - the torch restatement of the reference's TorchAttention.forward (fp32, the
                  host's cores) on a bounded sample of the same workload;
   secondary    - the other BASELINE configs (C1, C3 prefill TFLOP/s + decode GB/s, C4 on
@@ -208,6 +210,74 @@ def cpu_baseline(idx: int, budget_s: float, seed: int = 0) -> dict:
     }
 
 
+CALIB_ELEMS = 1 << 27  # bf16 elements of the calibration copy: 256 MiB read + 256 MiB written
+
+
+def pmc_child() -> None:
+    """Workload of one counter pass: a plain copy of known size (torch.neg on bf16: reads and
+    writes CALIB bytes, a kernel whose name holds "neg_kernel"), then C2 write + forwards."""
+    import torch
+
+    from kvserve_amd import HipAttention, workloads
+
+    x = torch.ones(CALIB_ELEMS, dtype=torch.bfloat16, device="cuda:0")
+    y = torch.empty_like(x)
+    for _ in range(2):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    del x, y
+    w = workloads.baseline_config(2)
+    b = workloads.materialize(w, torch.bfloat16, "cuda:0")
+    HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping)
+    for _ in range(3):
+        HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale)
+    torch.cuda.synchronize()
+
+
+def measure_traffic(timeout_s: int = 150) -> dict | None:
+    """HBM bytes per decode-kernel launch from two rocprofv3 --pmc passes (FETCH_SIZE, then
+    WRITE_SIZE, KiB per dispatch), each scaled by what the same counter reads for the
+    calibration copy of known size. None when rocprofv3 is missing or a pass fails."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not Path(prof).exists():
+        return None
+    calib_bytes = CALIB_ELEMS * 2
+    out = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="kvh_pmc_", dir="/tmp")
+        cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "pmc", "--",
+               sys.executable, str(ROOT / "bench.py"), "--pmc-child"]  # fmt: skip
+        env = dict(os.environ, TMPDIR="/tmp")
+        try:
+            subprocess.run(cmd, cwd="/tmp", env=env, timeout=timeout_s, check=True,
+                           stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)  # fmt: skip
+        except (subprocess.SubprocessError, OSError):
+            shutil.rmtree(d, ignore_errors=True)
+            return None
+        calib, dec = [], []
+        for f in Path(d).rglob("*counter_collection.csv"):
+            for row in csv.DictReader(open(f)):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name, val = row["Kernel_Name"], float(row["Counter_Value"]) * 1024.0
+                if "neg_kernel" in name:
+                    calib.append(val)
+                elif "pa_decode_kernel" in name:
+                    dec.append(val)
+        shutil.rmtree(d, ignore_errors=True)
+        if not calib or not dec:
+            return None
+        factor = statistics.mean(calib) / calib_bytes
+        out[counter] = {"raw_bytes": statistics.mean(dec), "calib_factor": factor,
+                        "bytes": statistics.mean(dec) / factor}  # fmt: skip
+    return out
+
+
 def main() -> int:
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -218,7 +288,12 @@ def main() -> int:
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", type=int, default=0, help="run just this config (1-5) and print its record")
+    p.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
+    p.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = p.parse_args()
+    if args.pmc_child:
+        pmc_child()
+        return 0
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -276,11 +351,24 @@ def main() -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": None,
-            "kernel": "pa_decode_kernel<BF16,128,1>",
+            "kernel": "pa_decode_kernel<BF16,128,1> (stream-K decode)",
             "kernel_ms": dec_ms,
         },
         "kernel_ms": head["kernel_ms"],
     }
+    if not args.no_traffic:
+        t = measure_traffic()
+        if t is not None:
+            rl = record["roofline"]
+            rl["traffic"] = t["FETCH_SIZE"]["bytes"] + t["WRITE_SIZE"]["bytes"]
+            rl["traffic_detail"] = {
+                "fetch_bytes": t["FETCH_SIZE"]["bytes"],
+                "write_bytes": t["WRITE_SIZE"]["bytes"],
+                "fetch_calib_factor": t["FETCH_SIZE"]["calib_factor"],
+                "write_calib_factor": t["WRITE_SIZE"]["calib_factor"],
+                "algorithmic_bytes": head["attn_bytes"],
+            }
+        print(f"# traffic: {t}", file=sys.stderr, flush=True)
     if not args.no_secondary:
         sec = {}
         for idx in (1, 3, 4, 5):
