@@ -55,17 +55,19 @@ Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t 
   pl.NT = (pl.QS * G + 15) / 16;
   pl.RS = pl.QS * G;
   pl.HGW = Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1);
-  pl.pre_rows_per_wg = 128;
-  pl.pre_tiles = (int32_t)(((int64_t)max_q * G + pl.pre_rows_per_wg - 1) / pl.pre_rows_per_wg);
   pl.slots = (int64_t)B * Hkv / pl.HGW + kMaxDecodeWaves / pl.HGW;
   if (dtype == KVH_DTYPE_F32) {
-    pl.ws_acc_bytes = pl.ws_ml_bytes = pl.ws_cum_bytes = pl.ws_bytes = 0;
+    pl.ws_acc_bytes = pl.ws_ml_bytes = pl.ws_job_bytes = pl.ws_pacc_bytes = pl.ws_pml_bytes = pl.ws_bytes = 0;
   } else {
     const size_t rows = (size_t)pl.slots * pl.HGW * pl.RS;
     pl.ws_acc_bytes = align_up(rows * D * sizeof(float));
     pl.ws_ml_bytes = align_up(rows * 2 * sizeof(float));
-    pl.ws_cum_bytes = align_up(((size_t)B + 1) * sizeof(int32_t));
-    pl.ws_bytes = pl.ws_acc_bytes + pl.ws_ml_bytes + pl.ws_cum_bytes;
+    const size_t jobs = kMaxDecodeWaves + (pl.launch_prefill ? kMaxPrefillUnits : 0);
+    pl.ws_job_bytes = align_up(jobs * kJobInts * sizeof(int32_t));
+    const size_t prows = pl.launch_prefill ? (size_t)2 * kMaxPrefillUnits * kPrefillRows : 0;
+    pl.ws_pacc_bytes = align_up(prows * D * sizeof(float));
+    pl.ws_pml_bytes = align_up(prows * 2 * sizeof(float));
+    pl.ws_bytes = pl.ws_acc_bytes + pl.ws_ml_bytes + pl.ws_job_bytes + pl.ws_pacc_bytes + pl.ws_pml_bytes;
   }
   (void)T;
   return pl;
@@ -130,6 +132,8 @@ static int check_attention_shape(int64_t num_tokens, int32_t num_seqs, int32_t n
     return KVH_E_SHAPE;
   if (num_heads % num_kv_heads != 0) return KVH_E_SHAPE;
   if (num_seqs > 65535 || num_heads > 65535 || num_tokens > 0x7fffffffLL) return KVH_E_UNSUPPORTED;
+  // query rows (token, head of a group) are indexed with 32-bit integers
+  if (num_tokens * (num_heads / num_kv_heads) > 0x7fffffffLL) return KVH_E_UNSUPPORTED;
   if ((int64_t)max_blocks_per_seq * block_size >= 0x7fffffffLL) return KVH_E_UNSUPPORTED;
   if (dtype == KVH_DTYPE_F32) {
     if (head_dim % 4 != 0 || head_dim > 256) return KVH_E_UNSUPPORTED;
@@ -225,10 +229,20 @@ int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stri
   p.QS = plan.QS;
   p.RS = plan.RS;
   p.HGW = plan.HGW;
-  p.NU = 0;  // set by the decode launcher from the device's occupancy
-  p.ws_acc = plan.ws_bytes ? (float*)workspace : nullptr;
-  p.ws_ml = plan.ws_bytes ? (float*)((char*)workspace + plan.ws_acc_bytes) : nullptr;
-  p.ws_cum = plan.ws_bytes ? (int32_t*)((char*)workspace + plan.ws_acc_bytes + plan.ws_ml_bytes) : nullptr;
+  p.NU = 0;   // set by the decode launcher from the device's occupancy
+  p.NUP = 0;  // set by the prefill launcher likewise
+  if (plan.ws_bytes) {
+    char* w = (char*)workspace;
+    p.ws_acc = (float*)w;
+    w += plan.ws_acc_bytes;
+    p.ws_ml = (float*)w;
+    w += plan.ws_ml_bytes;
+    p.ws_job = (int32_t*)w;
+    w += plan.ws_job_bytes;
+    p.ws_pacc = plan.ws_pacc_bytes ? (float*)w : nullptr;
+    w += plan.ws_pacc_bytes;
+    p.ws_pml = plan.ws_pml_bytes ? (float*)w : nullptr;
+  }
 
   hipStream_t s = (hipStream_t)stream;
   if (n_armed > 0) {

@@ -60,16 +60,21 @@ __device__ __forceinline__ uint32_t pick_halves(uint32_t a, uint32_t b) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Cross-lane reductions over the four 16-lane groups (lanes n, n+16, n+32, n+48).
+// Cross-lane reductions over the four 16-lane groups (lanes n, n+16, n+32, n+48) with the
+// CDNA4 VALU swaps (no LDS round trip). With both operands equal, v_permlane32_swap returns
+// {x[l % 32], x[l % 32 + 32]} and v_permlane16_swap returns the even and the odd 16-lane row
+// of each 32-lane half, so combining the pair reduces over lanes l ^ 32, then l ^ 16.
 __device__ __forceinline__ float max_over_groups(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float sum_over_groups(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 __device__ __forceinline__ int64_t clamp64(int64_t x, int64_t lo, int64_t hi) {

@@ -10,6 +10,13 @@ namespace kvh {
 // Upper bound on the waves one decode launch uses (256 CUs x 8 waves per SIMD x 4 SIMDs
 // would be 8192); the workspace is sized for it, so its size never depends on the device.
 constexpr int32_t kMaxDecodeWaves = 8192;
+// Upper bound on the workgroups (work units) of one prefill launch: 256 CUs x 2 resident.
+constexpr int32_t kMaxPrefillUnits = 512;
+// Query rows ((token, head) pairs of one kv head) one prefill workgroup owns.
+constexpr int32_t kPrefillRows = 128;
+// Merge job record: int32 fields, one record per work unit (decode units first).
+constexpr int32_t kJobInts = 16;
+constexpr int32_t kMaxJobs = kMaxDecodeWaves + kMaxPrefillUnits;
 
 // Everything a paged-attention kernel reads, by value in the kernel argument segment.
 // Strides are in elements; cache strides are {block, slot, head}.
@@ -35,20 +42,21 @@ struct PAParams {
   int32_t RS;      // query rows of a decode-class sequence at most: QS * G
   int32_t HGW;     // kv heads (waves) per work unit of the decode kernel: 4, 2 or 1
   int32_t NU;      // work units the decode launch provides (waves / HGW)
-  float* ws_acc;   // [slots, HGW, RS, D] unnormalised partial outputs of split segments
+  int32_t NUP;     // work units (workgroups) of the prefill launch, 0 when none
+  float* ws_acc;   // [slots, HGW, RS, D] unnormalised partial outputs of split decode segments
   float* ws_ml;    // [slots, HGW, RS, 2] running max (exp2 domain) and sum of each partial
-  int32_t* ws_cum; // [B + 1] prefix sums of decode chunks per kv head, written by the decode kernel
+  float* ws_pacc;  // [2 kMaxPrefillUnits, kPrefillRows, D] partial outputs of split prefill tiles
+  float* ws_pml;   // [2 kMaxPrefillUnits, kPrefillRows, 2]
+  int32_t* ws_job; // [kMaxJobs, kJobInts] merge jobs, rewritten by every unit on every call
 };
 
 // Launch plan: a pure function of static shapes (graph-capture safe).
 struct Plan {
   int32_t G, QS, NT, RS;    // GQA group, decode-class q_len cap, 16-row tiles, rows per sequence
   int32_t HGW;              // kv heads per decode work unit
-  int32_t pre_rows_per_wg;  // rows of one prefill workgroup
   bool launch_prefill;      // max_query_len > QS
-  int32_t pre_tiles;        // prefill workgroups per (seq, kv_head)
   int64_t slots;            // partial slots: B * Hkv / HGW + kMaxDecodeWaves / HGW
-  size_t ws_acc_bytes, ws_ml_bytes, ws_cum_bytes, ws_bytes;
+  size_t ws_acc_bytes, ws_ml_bytes, ws_job_bytes, ws_pacc_bytes, ws_pml_bytes, ws_bytes;
 };
 
 Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t W, int32_t BS, int32_t max_q,

@@ -60,12 +60,23 @@ __device__ __forceinline__ void load_window(PageWindow& pw, const PAParams& p, c
   pw.page0 = page0;
 }
 
-// Block id of `page` (wave-uniform), refreshing the window when the page leaves it.
+// Block id of `page` (wave-uniform), refreshing the window when the page leaves it. A
+// refresh keeps kWindowHistory pages below `page` so pages a few chunks behind (still being
+// computed while later chunks are loaded) stay readable with peek_block.
+constexpr int kWindowHistory = 8;
+
 __device__ __forceinline__ int page_block(PageWindow& pw, const PAParams& p, const int64_t* btrow, int page,
                                           int page_end) {
   if (page >= page_end) return -1;
-  if (page - pw.page0 >= 64 || page < pw.page0) load_window(pw, p, btrow, page, page_end);
+  if (page - pw.page0 >= 64 || page < pw.page0)
+    load_window(pw, p, btrow, page >= kWindowHistory ? page - kWindowHistory : 0, page_end);
   return __builtin_amdgcn_readlane(pw.ids, page - pw.page0);
+}
+
+// Block id of `page` if the window holds it, else -1 (no refresh, no memory access).
+__device__ __forceinline__ int peek_block(const PageWindow& pw, int page) {
+  const int rel = page - pw.page0;
+  return (rel >= 0 && rel < 64) ? __builtin_amdgcn_readlane(pw.ids, rel) : -1;
 }
 
 // Per-lane registers of one 32-token chunk of one kv head.
@@ -193,31 +204,36 @@ __device__ __forceinline__ void load_q(WaveState<D, NT>& s, const PAParams& p, i
 
 // Scores of one chunk and the online-softmax update; returns the P^T B operands.
 // MASKED = false only when every token of the chunk is visible to every valid row.
-template <class E, int D, int NT, bool MASKED>
+// LAZY: skip the accumulator rescale when no row max moved (a uniform branch; exact, and a
+// win for decode where the max settles early); otherwise the body is straight-line so the
+// row tiles' dependency chains interleave.
+template <class E, int D, int NT, bool MASKED, bool LAZY = true>
 __device__ __forceinline__ void chunk_scores(WaveState<D, NT>& s, const KRegs<D>& kr, const PAParams& p,
                                              const ChunkRef& c, u32x4 pt[NT]) {
   const int j = (threadIdx.x & 63) >> 4;
+  f32x4 st[NT][2];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    f32x4 st[2];
+  for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int tile = 0; tile < 2; ++tile) {
       f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int cc = 0; cc < D / 32; ++cc) a = E::mfma(kr.k[tile][cc], s.q[t][cc], a);
-      st[tile] = a;
+      st[t][tile] = a;
     }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
     float mx = -INFINITY;
 #pragma unroll
     for (int tile = 0; tile < 2; ++tile) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float x = st[tile][e] * p.qk_scale;
+        float x = st[t][tile][e] * p.qk_scale;
         if (MASKED) {
           const int tok = c.tok0 + 16 * tile + 4 * j + e;
           if (!(c.blk[tile] >= 0 && tok < s.limit[t])) x = -INFINITY;
         }
-        st[tile][e] = x;
+        st[t][tile][e] = x;
         mx = fmaxf(mx, x);
       }
     }
@@ -225,8 +241,7 @@ __device__ __forceinline__ void chunk_scores(WaveState<D, NT>& s, const KRegs<D>
     const float m_old = s.m[t];
     const float m_new = fmaxf(m_old, mx);
     const float m_safe = m_new == -INFINITY ? 0.f : m_new;
-    // Rescale only when some row's max moved: alpha is exactly 1 otherwise.
-    if (__builtin_amdgcn_ballot_w64(m_new > m_old)) {
+    if (!LAZY || __builtin_amdgcn_ballot_w64(m_new > m_old)) {
       const float alpha = fast_exp2(m_old - m_safe);
       s.l[t] *= alpha;
 #pragma unroll
@@ -238,7 +253,7 @@ __device__ __forceinline__ void chunk_scores(WaveState<D, NT>& s, const KRegs<D>
     for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float x = fast_exp2(st[tile][e] - m_safe);
+        const float x = fast_exp2(st[t][tile][e] - m_safe);
         pv[4 * tile + e] = x;
         psum += x;
       }
@@ -356,7 +371,8 @@ __device__ __forceinline__ SeqView seq_view(const PAParams& p, int seq) {
 // ws row index row_base + r. Lane (j, n) holds row row0 + 16t + n, d = VW (4j + e) + i.
 template <class E, int D, int NT>
 __device__ __forceinline__ void write_rows(const WaveState<D, NT>& s, const PAParams& p, const SeqView& sv, int R,
-                                           int row0, int kvh, bool partial, int64_t row_base) {
+                                           int row0, int kvh, bool partial, float* ws_acc, float* ws_ml,
+                                           int64_t row_base) {
   constexpr int VW = D / 16;
   const int lane = threadIdx.x & 63;
   const int j = lane >> 4, n = lane & 15;
@@ -378,7 +394,7 @@ __device__ __forceinline__ void write_rows(const WaveState<D, NT>& s, const PAPa
       }
     } else {
       const int64_t idx = row_base + r;
-      float* dst = p.ws_acc + idx * D;
+      float* dst = ws_acc + idx * D;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -386,11 +402,30 @@ __device__ __forceinline__ void write_rows(const WaveState<D, NT>& s, const PAPa
           *(f32x4*)(dst + VW * (4 * j + e) + i) =
               f32x4{s.acc[t][i][e], s.acc[t][i + 1][e], s.acc[t][i + 2][e], s.acc[t][i + 3][e]};
       if (j == 0) {
-        p.ws_ml[idx * 2] = s.m[t];
-        p.ws_ml[idx * 2 + 1] = L;
+        ws_ml[idx * 2] = s.m[t];
+        ws_ml[idx * 2 + 1] = L;
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------------------
+// Merge jobs. A split segment is merged by one workgroup of pa_merge_kernel, described by
+// the unit that computed its first piece: kind, number of pieces, slots of the pieces
+// (piece i lives in slot0 for i = 0, else in slotb + stride * i), and where its rows go.
+constexpr int32_t kJobNone = 0, kJobDecode = 1, kJobPrefill = 2;
+
+__device__ __forceinline__ void write_job(int32_t* job, int kind, int pieces, int64_t slot0, int64_t slotb,
+                                          int stride, int64_t qs, int R, int rbase, int kvh0) {
+  job[1] = pieces;
+  job[2] = (int32_t)slot0;
+  job[3] = (int32_t)slotb;
+  job[4] = stride;
+  job[5] = (int32_t)qs;  // flat token index: < 2^31 (validated)
+  job[6] = R;
+  job[7] = rbase;
+  job[8] = kvh0;
+  job[0] = kind;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -401,7 +436,7 @@ __device__ __forceinline__ void write_rows(const WaveState<D, NT>& s, const PAPa
 // chunks [u C / NU', (u + 1) C / NU'), NU' = min(NU, ceil(C / kMinUnitChunks)); the HGW
 // waves of a unit take the HGW heads of each segment, so they stream adjacent slices of the
 // same cache rows. A segment split between units leaves one partial per unit in slot
-// (segment index + unit), which pa_reduce_kernel merges.
+// (segment index + unit); the unit holding a split segment's first piece records a merge job.
 constexpr int kMinUnitChunks = 4;
 
 __device__ __forceinline__ int seq_chunks(const PAParams& p, int s) {
@@ -451,16 +486,19 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
   const int unit = gw / p.HGW, hw = gw % p.HGW;
   const int NHG = p.Hkv / p.HGW;
 
-  // Prefix sums of chunks per segment over all sequences (every wave computes them; the
-  // first wave also publishes them for the reduce kernel).
+  // This unit's merge job: none unless it owns a split segment (below). Written on every
+  // call, so the merge kernel never sees a stale record.
+  int32_t* job = p.ws_job + (int64_t)unit * kJobInts;
+  const bool job_writer = hw == 0 && lane == 0 && unit < p.NU;
+  if (job_writer) job[0] = kJobNone;
+
+  // Chunks per segment over all sequences (every wave computes the sum itself).
   int Cs = 0;
   for (int blk0 = 0; blk0 < p.B; blk0 += 64) {
     SeqWindow sw;
     scan_window(sw, p, blk0, Cs);
-    if (gw == 0 && blk0 + lane < p.B) p.ws_cum[blk0 + lane] = Cs + sw.excl;
     Cs += sw.total;
   }
-  if (gw == 0 && lane == 0) p.ws_cum[p.B] = Cs;
   const int64_t C = (int64_t)Cs * NHG;
   const int64_t NUa = active_units(C, p.NU);
   if (unit >= NUa) return;
@@ -495,112 +533,474 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
     run_chunks<E, D, NT>(st, p, btrow, kvh, tok_lo, kChunk, tok_hi, sv.kv_total);
     const bool whole = pos == seg_beg && y == seg_end;
     const int64_t slot = (int64_t)seq * NHG + hg + unit;
-    write_rows<E, D, NT>(st, p, sv, R, 0, kvh, !whole, (slot * p.HGW + hw) * p.RS);
+    write_rows<E, D, NT>(st, p, sv, R, 0, kvh, !whole, p.ws_acc, p.ws_ml, (slot * p.HGW + hw) * p.RS);
+    if (job_writer && pos == seg_beg && y < seg_end) {
+      // the segment starts here and continues in units unit + 1 .. u1: piece i is in slot + i
+      const int64_t u1 = (seg_end * NUa - 1) / C;
+      write_job(job, kJobDecode, (int)(u1 - unit + 1), slot, slot, 1, sv.qs, R, 0, hg * p.HGW);
+    }
     pos = y;
   }
 }
 
-// Log-sum-exp merge of the pieces of split decode segments. Grid (RS, Hkv, B): one wave per
-// query row; lane owns D / 64 consecutive elements. Units u0 .. u1 hold the pieces of the
-// row's segment [seg_beg, seg_end); a segment held by one unit was written out directly.
+// Log-sum-exp merge of split segments. A job covers `rows` partial rows per piece (HGW
+// heads x RS rows for decode, kPrefillRows rows of one head for prefill); row x of piece i
+// sits at (slot(i) * rows + x) in the partial arrays. Each workgroup merges 16 rows of one
+// job: workgroups 0 .. NU * CD - 1 take decode unit b / CD, rows 16 (b % CD) ..; the next
+// NUP * 8 take prefill record b' / 8, rows 16 (b' % 8) ... Thread t < 16 finds the max of
+// its row over the pieces and stages the pieces' weights in LDS, 16 pieces at a time; then
+// every thread accumulates F = D / 64 float4 of the 16 rows with the piece loop unrolled,
+// so the loads of several pieces are in flight together. Rows are normalised at the store.
+constexpr int kMergeBatch = 16;
+constexpr int kMergeRows = 16;
+
+__device__ __forceinline__ int merge_chunks_decode(const PAParams& p) {
+  return (p.HGW * p.RS + kMergeRows - 1) / kMergeRows;
+}
+
 template <class E, int D>
-__global__ __launch_bounds__(64) void pa_reduce_kernel(PAParams p) {
-  constexpr int PL = D / 64;  // elements per lane
-  const int r = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
-  const int lane = threadIdx.x;
-  const SeqView sv = seq_view(p, seq);
-  if (sv.q_len == 0 || sv.q_len > p.QS) return;
-  if (r >= sv.q_len * p.G) return;
-  const int NHG = p.Hkv / p.HGW;
-  const int hg = kvh / p.HGW, hw = kvh % p.HGW;
-  const int c = max(1, (sv.kv_total + kChunk - 1) / kChunk);
-  const int64_t C = (int64_t)p.ws_cum[p.B] * NHG;
-  const int64_t NUa = active_units(C, p.NU);
-  const int64_t seg_beg = (int64_t)p.ws_cum[seq] * NHG + (int64_t)hg * c, seg_end = seg_beg + c;
-  const int64_t u0 = ((seg_beg + 1) * NUa - 1) / C, u1 = (seg_end * NUa - 1) / C;
-  if (u0 == u1) return;
-  const int64_t seg = (int64_t)seq * NHG + hg;
-  auto row = [&](int64_t u) { return ((seg + u) * p.HGW + hw) * p.RS + r; };
-  float M = -INFINITY;
-  for (int64_t u = u0; u <= u1; ++u) M = fmaxf(M, p.ws_ml[row(u) * 2]);
-  const float msafe = M == -INFINITY ? 0.f : M;
-  float L = 0.f;
-  float o[PL];
+__global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
+  constexpr int Q4 = D / 4;                    // float4 per row
+  constexpr int F = kMergeRows * Q4 / 256;     // float4 per thread
+  __shared__ float s_w[kMergeRows][kMergeBatch + 1];
+  __shared__ float s_inv[kMergeRows];
+  const int CD = merge_chunks_decode(p);
+  const int b = blockIdx.x;
+  int64_t jidx;
+  int chunk;
+  if (b < p.NU * CD) {
+    jidx = b / CD;
+    chunk = b % CD;
+  } else {
+    const int bp = b - p.NU * CD;
+    jidx = (int64_t)kMaxDecodeWaves + bp / (kPrefillRows / kMergeRows);
+    chunk = bp % (kPrefillRows / kMergeRows);
+  }
+  const int32_t* job = p.ws_job + jidx * kJobInts;
+  const int kind = job[0];
+  if (kind == kJobNone) return;
+  const bool dec = kind == kJobDecode;
+  const int rows = dec ? p.HGW * p.RS : kPrefillRows;
+  const int x0 = chunk * kMergeRows;
+  if (x0 >= rows) return;
+  const int nr = min(kMergeRows, rows - x0);
+  const int pieces = job[1];
+  const int64_t slot0 = job[2], slotb = job[3];
+  const int stride = job[4];
+  const int64_t qs = job[5];
+  const int R = job[6], rbase = job[7], kvh0 = job[8];
+  const int rph = dec ? p.RS : kPrefillRows;  // rows per head
+  const float* acc = dec ? p.ws_acc : p.ws_pacc;
+  const float* ml = dec ? p.ws_ml : p.ws_pml;
+  auto slot = [&](int i) -> int64_t { return i == 0 ? slot0 : slotb + (int64_t)stride * i; };
+  const int t = threadIdx.x;
+
+  float msafe = 0.f, L = 0.f;
+  if (t < nr) {
+    float M = -INFINITY;
+#pragma unroll 8
+    for (int i = 0; i < pieces; ++i) M = fmaxf(M, ml[(slot(i) * rows + x0 + t) * 2]);
+    msafe = M == -INFINITY ? 0.f : M;
+  }
+  const int nq = nr * Q4;
+  int qc[F];
 #pragma unroll
-  for (int i = 0; i < PL; ++i) o[i] = 0.f;
+  for (int f = 0; f < F; ++f) qc[f] = min(t + 256 * f, nq - 1);  // clamped: loads stay in the rows
+  f32x4 o[F];
+#pragma unroll
+  for (int f = 0; f < F; ++f) o[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i0 = 0; i0 < pieces; i0 += kMergeBatch) {
+    __syncthreads();
+    if (t < nr) {
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) {
+        const int i = i0 + k;
+        float w = 0.f;
+        if (i < pieces) {
+          const float2 x = *(const float2*)(ml + (slot(i) * rows + x0 + t) * 2);
+          w = fast_exp2(x.x - msafe);
+          L += w * x.y;
+        }
+        s_w[t][k] = w;
+      }
+    }
+    __syncthreads();
+    const int ni = min(kMergeBatch, pieces - i0);
 #pragma unroll 4
-  for (int64_t u = u0; u <= u1; ++u) {
-    const int64_t idx = row(u);
-    const float f = fast_exp2(p.ws_ml[idx * 2] - msafe);
-    L += f * p.ws_ml[idx * 2 + 1];
-    const float* acc = p.ws_acc + idx * D + PL * lane;
-    if constexpr (PL == 2) {
-      const float2 x = *(const float2*)acc;
-      o[0] += f * x.x;
-      o[1] += f * x.y;
-    } else {
-      o[0] += f * acc[0];
+    for (int k = 0; k < ni; ++k) {
+      const float* src = acc + (slot(i0 + k) * rows + x0) * D;
+#pragma unroll
+      for (int f = 0; f < F; ++f) o[f] += s_w[qc[f] / Q4][k] * *(const f32x4*)(src + 4 * qc[f]);
     }
   }
-  const float inv = 1.f / (L == 0.f ? 1.f : L);
-  const int qi = r / p.G, g = r % p.G;
-  uint16_t* dst = (uint16_t*)p.out + (sv.qs + qi) * p.o_ts + (int64_t)(kvh * p.G + g) * p.o_hs + PL * lane;
-  if constexpr (PL == 2) {
-    *(uint32_t*)dst = E::pack2(o[0] * inv, o[1] * inv);
-  } else {
-    *dst = (uint16_t)(E::pack2(o[0] * inv, 0.f) & 0xffffu);
+  if (t < nr) s_inv[t] = 1.f / (L == 0.f ? 1.f : L);
+  __syncthreads();
+#pragma unroll
+  for (int f = 0; f < F; ++f) {
+    const int q = t + 256 * f;
+    if (q >= nq) continue;
+    const int xr = q / Q4, col = 4 * (q % Q4);
+    const int x = x0 + xr;
+    const int hw = x / rph, r = rbase + x % rph;
+    if (r >= R) continue;
+    const float inv = s_inv[xr];
+    uint16_t* dst = (uint16_t*)p.out + (qs + r / p.G) * p.o_ts + (int64_t)((kvh0 + hw) * p.G + r % p.G) * p.o_hs + col;
+    *(u32x2*)dst = u32x2{E::pack2(o[f][0] * inv, o[f][1] * inv), E::pack2(o[f][2] * inv, o[f][3] * inv)};
   }
 }
 
 // ---------------------------------------------------------------------------------------
-// Prefill class: grid (ceil(max_q * G / 128), Hkv, B); wave w owns rows
-// (blockIdx.x * 4 + w) * 32 .. + 31 of its sequence's R = q_len * G rows.
-template <class E, int D>
-__global__ __launch_bounds__(256) void pa_prefill_kernel(PAParams p) {
-  constexpr int NT = kPrefillNQT;
-  const int kvh = blockIdx.y, seq = blockIdx.z;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+// Prefill class (q_len > QS): a workgroup of 4 waves computes kPrefillRows = 128 query rows
+// of one (sequence, kv head), wave w holding rows 32 w .. 32 w + 31 of the tile.
+//
+// The 4 waves share every 32-key K/V chunk through a 3-stage LDS ring filled by direct
+// global->LDS loads (no VGPR staging): chunk c + 2 is in flight while chunk c is computed.
+// Each 16-byte slot s of LDS row t holds the row's global slot s ^ (t % slots_per_row), so
+// both the K-operand reads (16 rows, one slot) and the V-operand reads (4 rows, 16 slots)
+// hit 16 distinct bank groups. Waves wait with s_waitcnt on their own loads, then a bare
+// s_barrier makes all four waves' loads of the chunk visible.
+template <int D>
+struct PrefillLds {
+  static constexpr int kRowBytes = D * 2;                // one token row of one kv head
+  static constexpr int kSlots = kRowBytes / 16;          // 16-byte slots per row
+  static constexpr int kRowsPerLoad = 1024 / kRowBytes;  // rows one wave-wide load fills
+  static constexpr int kTileBytes = kChunk * kRowBytes;  // K (or V) of one chunk
+  static constexpr int kLoadsPerTile = kTileBytes / 1024;
+  static constexpr int kLoadsPerWave = 2 * kLoadsPerTile / kWavesPerWG;  // K and V, split over 4 waves
+  static constexpr int kStages = 3;
+  static constexpr int kStageBytes = 2 * kTileBytes;
+};
 
-  const SeqView sv = seq_view(p, seq);
-  if (sv.q_len <= p.QS) return;
-  const int R = sv.q_len * p.G;
-  const int row0 = (blockIdx.x * kWavesPerWG + w) * (16 * NT);
-  if (row0 >= R) return;
-  const int last_row = min(row0 + 16 * NT - 1, R - 1);
-  const int kv_lim = (int)clamp64(sv.ctx + last_row / p.G + 1, 0, sv.kv_total);
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// This wave's share of the direct loads of chunk `tok0` into ring stage `stage`.
+template <int D>
+__device__ __forceinline__ void prefill_issue(char* lds, int stage, const PAParams& p, PageWindow& pw,
+                                              const int64_t* btrow, int kvh, int tok0, int page_end, int w) {
+  using L = PrefillLds<D>;
+  const int lane = threadIdx.x & 63;
+  const int row_in = lane / L::kSlots, slot = lane % L::kSlots;
+#pragma unroll
+  for (int k = 0; k < L::kLoadsPerWave; ++k) {
+    const int g = w * L::kLoadsPerWave + k;  // 0 .. 2 * kLoadsPerTile - 1
+    const int which = g / L::kLoadsPerTile;  // 0: K, 1: V
+    const int i = g % L::kLoadsPerTile;
+    const int row0 = i * L::kRowsPerLoad;    // the load's rows share one page (BS % 16 == 0)
+    const int tok = tok0 + row0;
+    int blk = page_block(pw, p, btrow, tok / p.BS, page_end);
+    if (blk < 0) blk = 0;                    // absent page: read block 0, masked later
+    const int row = row0 + row_in;
+    const int64_t sb = which ? p.v_sb : p.k_sb, ss = which ? p.v_ss : p.k_ss, sh = which ? p.v_sh : p.k_sh;
+    const char* base = (const char*)(which ? p.vc : p.kc);
+    const char* src = base + ((int64_t)blk * sb + (int64_t)((tok % p.BS) + row_in) * ss + (int64_t)kvh * sh) * 2 +
+                      16 * (slot ^ (row % L::kSlots));
+    char* dst = lds + stage * L::kStageBytes + which * L::kTileBytes + i * 1024;
+    __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)dst, 16, 0, 0);
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void prefill_read_k(KRegs<D>& r, const char* tile) {
+  using L = PrefillLds<D>;
+  const int lane = threadIdx.x & 63;
+  const int j = lane >> 4, n = lane & 15;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int row = 16 * t + n;
+#pragma unroll
+    for (int cc = 0; cc < D / 32; ++cc) {
+      const int gslot = (D / 32) * j + cc;  // global 16-byte slot: d = (D/4) j + 8 cc
+      r.k[t][cc] = *(const u32x4*)(tile + row * L::kRowBytes + 16 * (gslot ^ (row % L::kSlots)));
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void prefill_read_v(VRegs<D>& r, const char* tile) {
+  using L = PrefillLds<D>;
+  constexpr int VW = D / 16;  // elements per lane per token: d = VW m ..
+  const int lane = threadIdx.x & 63;
+  const int j = lane >> 4, m = lane & 15;
+#pragma unroll
+  for (int t8 = 0; t8 < 8; ++t8) {
+    const int row = 16 * (t8 >> 2) + 4 * j + (t8 & 3);
+    const int byte = VW * m * 2;  // within the global row
+    const char* src = tile + row * L::kRowBytes + 16 * ((byte / 16) ^ (row % L::kSlots)) + byte % 16;
+    if constexpr (VW == 8) {
+      const u32x4 x = *(const u32x4*)src;
+      r.v[t8][0] = x[0];
+      r.v[t8][1] = x[1];
+      r.v[t8][2] = x[2];
+      r.v[t8][3] = x[3];
+    } else {
+      const u32x2 x = *(const u32x2*)src;
+      r.v[t8][0] = x[0];
+      r.v[t8][1] = x[1];
+    }
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  // s_waitcnt vmcnt(N), expcnt/lgkmcnt left free (gfx9 encoding)
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// One workgroup's pass over chunks [c_lo, c_hi) of tile t of (seq, kvh): the whole tile
+// (written out) or a piece of it (partial in slot `slot` of the prefill partial arrays).
+template <class E, int D>
+__device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const SeqView& sv, int R, int seq,
+                                             int kvh, int t, int c_lo, int c_hi, int w, bool partial,
+                                             int64_t slot) {
+  constexpr int NT = kPrefillNQT;
+  using L = PrefillLds<D>;
+  const int wg_row0 = t * kPrefillRows;
+  const int wg_last = min(wg_row0 + kPrefillRows - 1, R - 1);
+  const int kv_lim = (int)clamp64(sv.ctx + wg_last / p.G + 1, 0, sv.kv_total);
+  const int row0 = wg_row0 + w * 16 * NT;
+  const int my_last = min(row0 + 16 * NT - 1, R - 1);
+  const int my_lim = row0 < R ? (int)clamp64(sv.ctx + my_last / p.G + 1, 0, sv.kv_total) : 0;
 
   WaveState<D, NT> s;
   load_q<D, NT>(s, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
   const int64_t* btrow = p.bt + (int64_t)seq * p.bt_rs;
-  run_chunks<E, D, NT>(s, p, btrow, kvh, 0, kChunk, kv_lim, sv.kv_total);
-  write_rows<E, D, NT>(s, p, sv, R, row0, kvh, false, 0);
+  const int page_end = (kv_lim + p.BS - 1) / p.BS;
+  PageWindow pw;
+  load_window(pw, p, btrow, c_lo * kChunk / p.BS, page_end);
+
+  // every wave has finished reading the ring (previous tile) before it is refilled
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  const int n = c_hi - c_lo;
+  if (n > 0) prefill_issue<D>(lds, 0, p, pw, btrow, kvh, c_lo * kChunk, page_end, w);
+  if (n > 1) prefill_issue<D>(lds, 1, p, pw, btrow, kvh, (c_lo + 1) * kChunk, page_end, w);
+  for (int i = 0; i < n; ++i) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + 1 < n)
+      wait_vm<L::kLoadsPerWave>();  // chunk i + 1 may stay in flight
+    else
+      wait_vm<0>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + 2 < n)
+      prefill_issue<D>(lds, (i + 2) % L::kStages, p, pw, btrow, kvh, (c_lo + i + 2) * kChunk, page_end, w);
+    __builtin_amdgcn_sched_barrier(0);
+    const int tok0 = (c_lo + i) * kChunk;
+    if (tok0 < my_lim) {
+      const char* st = lds + (i % L::kStages) * L::kStageBytes;
+      ChunkRef cr;
+      cr.tok0 = tok0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int tt = tok0 + 16 * h;
+        cr.blk[h] = tt < kv_lim ? peek_block(pw, tt / p.BS) : -1;
+      }
+      KRegs<D> kr;
+      VRegs<D> vr;
+      prefill_read_k<D>(kr, st);
+      prefill_read_v<D>(vr, st + L::kTileBytes);
+      u32x4 pt[NT];
+      chunk_scores<E, D, NT, true, false>(s, kr, p, cr, pt);
+      chunk_pv<E, D, NT, true>(s, vr, cr, sv.kv_total, pt);
+    }
+  }
+  write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, p.ws_pacc, p.ws_pml, slot * kPrefillRows - wg_row0);
+}
+
+// Chunks of tile t (rows 128 t .. of R): those its last row can see, at least one so that
+// every tile is visited and written.
+__device__ __forceinline__ int pre_tile_chunks(const PAParams& p, const SeqView& sv, int R, int t) {
+  const int last = min(kPrefillRows * t + kPrefillRows - 1, R - 1);
+  const int lim = (int)clamp64(sv.ctx + last / p.G + 1, 0, sv.kv_total);
+  return max(1, (lim + kChunk - 1) / kChunk);
+}
+
+// Chunks of all tiles of one kv head of a prefill-class sequence; 0 for other sequences.
+__device__ __forceinline__ int64_t pre_seq_chunks(const PAParams& p, const SeqView& sv) {
+  if (sv.q_len <= p.QS) return 0;
+  const int R = sv.q_len * p.G;
+  const int tiles = (R + kPrefillRows - 1) / kPrefillRows;
+  int64_t n = 0;
+  for (int t = 0; t < tiles; ++t) n += pre_tile_chunks(p, sv, R, t);
+  return n;
+}
+
+__device__ __forceinline__ int64_t readlane64(int64_t x, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)x, l);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)x >> 32), l);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Inclusive prefix sum over the 64 lanes; `total` gets the uniform sum.
+__device__ __forceinline__ int64_t wave_scan64(int64_t x, int64_t& total) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  total = readlane64(x, 63);
+  return x;
+}
+
+// 64 consecutive sequences of the prefill flat space; lane l describes sequence blk0 + l.
+struct PreWindow {
+  int blk0;
+  int64_t base;   // flat chunks of all sequences before blk0
+  int64_t c;      // this lane's sequence: Hkv x its chunks per kv head
+  int64_t excl;   // flat chunks of sequences blk0 .. blk0 + l - 1
+  int64_t total;  // the whole window
+};
+
+__device__ __forceinline__ void pre_window(PreWindow& w, const PAParams& p, int blk0, int64_t base) {
+  const int s = blk0 + (threadIdx.x & 63);
+  w.blk0 = blk0;
+  w.base = base;
+  w.c = s < p.B ? (int64_t)p.Hkv * pre_seq_chunks(p, seq_view(p, s)) : 0;
+  w.excl = wave_scan64(w.c, w.total) - w.c;
+}
+
+// Stream-K over the prefill-class work: a flat space of (sequence, kv head, tile, chunk),
+// sequence-major, in which tile t of (seq, kvh) contributes pre_tile_chunks chunks. The
+// launch has one workgroup per resident slot (NUP, a multiple of 8); NUa = min(NUP,
+// ceil(C / kMinUnitChunks)) of them are work units, unit u taking chunks [u C / NUa,
+// (u + 1) C / NUa), so every unit does the same number of chunk steps whatever the mix of
+// prompt lengths, and none is empty. A tile split between units leaves partials: unit u
+// keeps the piece of its first tile in slot 2u and of its last tile in slot 2u + 1 (tiles
+// in between are whole and written out), and the unit holding a split tile's first piece
+// records its merge job (in the record of its workgroup). Workgroups are dealt to the 8
+// XCDs round-robin, so the units are numbered XCD by XCD: the units of one XCD are
+// contiguous in the flat space and read the same sequence's K/V through that XCD's L2.
+template <class E, int D>
+__global__ __launch_bounds__(256, 2) void pa_prefill_kernel(PAParams p) {
+  using L = PrefillLds<D>;
+  __shared__ __attribute__((aligned(1024))) char lds[L::kStages * L::kStageBytes];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int32_t* job = p.ws_job + (int64_t)(kMaxDecodeWaves + blockIdx.x) * kJobInts;
+  if (threadIdx.x == 0) job[0] = kJobNone;
+
+  // Flat size C: lane l sums the sequences l K .. l K + K - 1, then one wave scan.
+  const int K = (p.B + 63) / 64;
+  int64_t mine = 0;
+  for (int i = 0; i < K; ++i) {
+    const int sq = lane * K + i;
+    if (sq < p.B) mine += (int64_t)p.Hkv * pre_seq_chunks(p, seq_view(p, sq));
+  }
+  int64_t C;
+  const int64_t incl = wave_scan64(mine, C);
+  if (C == 0) return;
+  const int NUa = (int)active_units(C, p.NUP);
+  const int xcd = (int)(blockIdx.x % 8), j = (int)(blockIdx.x / 8);
+  const int q8 = NUa / 8, r8 = NUa % 8;
+  if (j >= q8 + (xcd < r8 ? 1 : 0)) return;  // idle workgroup (workgroup-uniform)
+  const int u = xcd * q8 + min(xcd, r8) + j;
+  const int64_t x0 = u * C / NUa, x1 = (u + 1) * C / NUa;
+  if (x0 >= x1) return;  // cannot happen: NUa <= C
+
+  // The window of 64 sequences from the block holding x0, then the sequence itself.
+  const uint64_t blk_hit = __builtin_amdgcn_ballot_w64(mine > 0 && incl - mine <= x0 && x0 < incl);
+  if (blk_hit == 0) return;  // cannot happen for consistent metadata
+  const int lb = __builtin_ctzll(blk_hit);
+  PreWindow win;
+  pre_window(win, p, lb * K, readlane64(incl - mine, lb));
+  int64_t x = x0;
+  int li = -1;
+  for (;;) {
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(win.c > 0 && win.base + win.excl <= x &&
+                                                     x < win.base + win.excl + win.c);
+    if (hit) {
+      li = __builtin_ctzll(hit);
+      break;
+    }
+    if (win.blk0 + 64 >= p.B) return;  // cannot happen for consistent metadata
+    pre_window(win, p, win.blk0 + 64, win.base + win.total);
+  }
+  int seq = win.blk0 + li;
+  SeqView sv = seq_view(p, seq);
+  int R = sv.q_len * p.G;
+  int tiles = (R + kPrefillRows - 1) / kPrefillRows;
+  int64_t per_kvh = readlane64(win.c, li) / p.Hkv;
+  const int64_t off = x - (win.base + readlane64(win.excl, li));
+  int kvh = (int)(off / per_kvh);
+  int64_t rem = off % per_kvh;
+  int t = 0;
+  int n_t = pre_tile_chunks(p, sv, R, 0);
+  while (rem >= n_t) {
+    rem -= n_t;
+    ++t;
+    n_t = pre_tile_chunks(p, sv, R, t);
+  }
+  int c_lo = (int)rem;
+  bool first = true;
+  for (;;) {
+    const int c_hi = (int)min((int64_t)n_t, c_lo + (x1 - x));
+    const bool whole = c_lo == 0 && c_hi == n_t;
+    const int64_t slot = 2 * (int64_t)u + (first ? 0 : 1);
+    prefill_tile<E, D>(lds, p, sv, R, seq, kvh, t, c_lo, c_hi, w, !whole, slot);
+    if (threadIdx.x == 0 && c_lo == 0 && c_hi < n_t) {
+      // the tile continues in units u + 1 .. u1, each holding it as its first tile
+      const int64_t x_last = x + (n_t - c_lo) - 1;
+      const int64_t u1 = ((x_last + 1) * NUa - 1) / C;
+      write_job(job, kJobPrefill, (int)(u1 - u + 1), slot, 2 * (int64_t)u, 2, sv.qs, R, t * kPrefillRows, kvh);
+    }
+    x += c_hi - c_lo;
+    if (x >= x1) break;
+    first = false;
+    c_lo = 0;
+    if (++t == tiles) {
+      t = 0;
+      if (++kvh == p.Hkv) {
+        kvh = 0;
+        // next sequence with prefill work
+        uint64_t nxt = __builtin_amdgcn_ballot_w64(win.c > 0) & (li < 63 ? ~0ull << (li + 1) : 0ull);
+        while (nxt == 0) {
+          if (win.blk0 + 64 >= p.B) return;  // cannot happen for consistent metadata
+          pre_window(win, p, win.blk0 + 64, win.base + win.total);
+          nxt = __builtin_amdgcn_ballot_w64(win.c > 0);
+        }
+        li = __builtin_ctzll(nxt);
+        seq = win.blk0 + li;
+        sv = seq_view(p, seq);
+        R = sv.q_len * p.G;
+        tiles = (R + kPrefillRows - 1) / kPrefillRows;
+        per_kvh = readlane64(win.c, li) / p.Hkv;
+      }
+    }
+    n_t = pre_tile_chunks(p, sv, R, t);
+  }
+  (void)per_kvh;
 }
 
 // ---------------------------------------------------------------------------------------
-// Waves one decode launch can keep resident on the current device, from the occupancy of
-// the instantiation actually launched (cached per device and kernel).
-static int resident_waves(const void* kernel) {
+// Workgroups of 256 threads one launch of `kernel` can keep resident on the current device
+// (cached per device and kernel).
+static int resident_blocks(const void* kernel) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 256 * kWavesPerWG;
-  static thread_local int cache_dev = -1;
-  static thread_local const void* cache_kernel = nullptr;
-  static thread_local int cache_waves = 0;
-  if (dev == cache_dev && kernel == cache_kernel) return cache_waves;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  struct Entry {
+    int dev;
+    const void* kernel;
+    int blocks;
+  };
+  static thread_local Entry cache[8];
+  static thread_local int cache_n = 0;
+  for (int i = 0; i < cache_n; ++i)
+    if (cache[i].dev == dev && cache[i].kernel == kernel) return cache[i].blocks;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu <= 0) per_cu = 1;
-  int waves = cus * per_cu * kWavesPerWG;
-  if (waves > kMaxDecodeWaves) waves = kMaxDecodeWaves;
-  cache_dev = dev;
-  cache_kernel = kernel;
-  cache_waves = waves;
-  return waves;
+  const int blocks = cus * per_cu;
+  if (cache_n < 8) cache[cache_n++] = Entry{dev, kernel, blocks};
+  return blocks;
 }
 
 template <class E, int D, int NT>
 static int launch_decode_nt(PAParams& p, hipStream_t s) {
   const void* k = (const void*)&pa_decode_kernel<E, D, NT>;
-  const int waves = resident_waves(k);
+  int waves = resident_blocks(k) * kWavesPerWG;
+  if (waves > kMaxDecodeWaves) waves = kMaxDecodeWaves;
   p.NU = waves / p.HGW;
   const int wgs = (p.NU * p.HGW + kWavesPerWG - 1) / kWavesPerWG;
   hipLaunchKernelGGL((pa_decode_kernel<E, D, NT>), dim3(wgs), dim3(256), 0, s, p);
@@ -610,6 +1010,13 @@ static int launch_decode_nt(PAParams& p, hipStream_t s) {
 template <class E, int D>
 static int launch_mfma_typed(PAParams& p, const Plan& plan, hipStream_t s, LaunchLog& log) {
   int err = 0;
+  if (plan.launch_prefill) {
+    // the unit count is fixed before the decode launch: both kernels write merge jobs
+    int units = resident_blocks((const void*)&pa_prefill_kernel<E, D>);
+    if (units > kMaxPrefillUnits) units = kMaxPrefillUnits;
+    p.NUP = units / 8 * 8;
+    if (p.NUP < 8) p.NUP = 8;
+  }
   switch (plan.NT) {
     case 1: err = launch_decode_nt<E, D, 1>(p, s); break;
     case 2: err = launch_decode_nt<E, D, 2>(p, s); break;
@@ -620,13 +1027,13 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, hipStream_t s, Launc
   if (err) return err;
   log.after_launch(1, s);
   if (plan.launch_prefill) {
-    dim3 grid(plan.pre_tiles, p.Hkv, p.B);
-    hipLaunchKernelGGL((pa_prefill_kernel<E, D>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((pa_prefill_kernel<E, D>), dim3(p.NUP), dim3(256), 0, s, p);
     if ((err = (int)hipGetLastError())) return err;
     log.after_launch(2, s);
   }
-  dim3 grid(plan.RS, p.Hkv, p.B);
-  hipLaunchKernelGGL((pa_reduce_kernel<E, D>), grid, dim3(64), 0, s, p);
+  const int cd = (p.HGW * p.RS + kMergeRows - 1) / kMergeRows;
+  const dim3 mg(p.NU * cd + p.NUP * (kPrefillRows / kMergeRows));
+  hipLaunchKernelGGL((pa_merge_kernel<E, D>), mg, dim3(256), 0, s, p);
   if ((err = (int)hipGetLastError())) return err;
   log.after_launch(3, s);
   return 0;

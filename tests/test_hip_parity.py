@@ -190,6 +190,40 @@ def test_mixed_batch_dispatch(hip_device):
     assert "prefill" not in last_launch_kernels()
 
 
+@pytest.mark.parametrize(
+    ("heads", "q_lens", "ctx_lens"),
+    [
+        ((32, 8), [1, 130, 3, 700, 33, 1], [50, 0, 4000, 1000, 3000, 9]),  # G=4, ragged tiles
+        ((16, 16), [65, 1, 200], [0, 300, 2500]),  # G=1: prefill from 17 queries per sequence
+        ((32, 2), [8, 1], [30_000, 70]),  # G=16: one tile per kv head, split over ~256 units
+        ((32, 4), [4096], [0]),  # one long prompt, causal from key 0
+    ],
+    ids=["g4_ragged", "g1", "g16_long_ctx", "g8_long_prompt"],
+)
+def test_prefill_stream_k(hip_device, heads, q_lens, ctx_lens):
+    """Prefill-class sequences go through the stream-K prefill kernel: tiles cut between
+    work units (including tiles merged from more than 16 pieces) match the oracle."""
+    H, Hkv = heads
+    w = workloads.custom("pre_sk", q_lens, ctx_lens, H, Hkv, 128, 16, seed=7)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=7)
+    out = pc.attend(b)
+    kinds = last_launch_kernels()
+    assert "prefill" in kinds and "reduce" in kinds, kinds
+    assert torch.isfinite(out.float()).all()
+    err = pc.max_err_vs_oracle(b, out, list(range(len(q_lens))), rows_per_seq=16)
+    assert err <= pc.TOL_16BIT, err
+
+
+def test_prefill_is_deterministic(hip_device):
+    """Two calls on the same inputs give bit-identical outputs (fixed unit ranges and merge
+    order; no atomics)."""
+    w = workloads.custom("pre_det", [300, 1, 77], [2000, 500, 0], 32, 8, 128, 16, seed=8)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=8)
+    o1 = pc.attend(b)
+    o2 = HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale)
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+
+
 def test_rows_without_keys_write_zeros(hip_device):
     """seq_len < q_len leaves early rows with no visible key: they come out as zeros (the
     reference divides by l = 0 -> 1, kernels/paged_attention.py:113)."""

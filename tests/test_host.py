@@ -81,6 +81,7 @@ def _call(lib, a):
         (dict(ws=0, ws_bytes=0), E_WORKSPACE),  # C2 needs split-K scratch
         (dict(dtype=0, D=102), E_UNSUPPORTED),
         (dict(B=70_000), E_UNSUPPORTED),
+        (dict(T=600_000_000), E_UNSUPPORTED),  # query rows T * G past 2^31
     ],
 )
 def test_attention_validation(lib, over, status):
@@ -107,20 +108,24 @@ def test_cache_write_validation(lib):
 
 
 def test_workspace_follows_the_plan(lib):
-    """Partial slots: one per (sequence, head group) plus one per possible decode work unit
-    (8192 waves / 4 heads per unit), each holding RS = QS * G rows; plus the chunk prefix sums."""
+    """Decode partial slots: one per (sequence, head group) plus one per possible decode work
+    unit (8192 waves / 4 heads per unit), each holding RS = QS * G rows; merge-job records
+    (16 int32) for 8192 decode units, plus 512 prefill units and their two 128-row partial
+    slots each when the batch has prefill-class queries."""
     ws = lib.kvh_paged_attention_workspace_size
 
-    def want(B, Hkv, G, QS, D, hgw=4):
+    def want(B, Hkv, G, QS, D, hgw=4, prefill=False):
         slots = B * Hkv // hgw + 8192 // hgw
         rows = slots * hgw * QS * G
         up = lambda x: -(-x // 256) * 256  # noqa: E731
-        return up(rows * D * 4) + up(rows * 2 * 4) + up((B + 1) * 4)
+        jobs = 8192 + (512 if prefill else 0)
+        prows = 2 * 512 * 128 if prefill else 0
+        return up(rows * D * 4) + up(rows * 2 * 4) + up(jobs * 16 * 4) + up(prows * D * 4) + up(prows * 2 * 4)
 
     assert ws(8, 8, 32, 8, 64, 32, 16, 1, 2) == want(8, 8, 4, 1, 64)  # C1
     assert ws(64, 64, 32, 8, 128, 512, 16, 1, 2) == want(64, 8, 4, 1, 128)  # C2
     assert ws(160, 32, 32, 8, 128, 257, 16, 5, 2) == want(32, 8, 4, 5, 128)  # C5: verify rows
-    assert ws(2048, 516, 32, 8, 128, 280, 16, 384, 2) == want(516, 8, 4, 4, 128)  # C3: QS = 16 / G
+    assert ws(2048, 516, 32, 8, 128, 280, 16, 384, 2) == want(516, 8, 4, 4, 128, prefill=True)  # C3
     assert ws(8, 8, 16, 2, 64, 32, 16, 1, 2) == want(8, 2, 8, 1, 64, hgw=2)  # two kv heads
     assert ws(64, 64, 32, 8, 128, 512, 16, 1, 0) == 0  # fp32 path: no split
     assert ws(64, 64, 30, 8, 128, 512, 16, 1, 2) == 0  # invalid shape
