@@ -30,6 +30,8 @@
 //    wave streams every key its rows can see (causal limit of its last row).
 // Grids depend only on static shapes (block-table width, max_query_len), never on
 // per-step lengths, so every launch is HIP-graph capturable.
+#include <type_traits>
+
 #include "kvh_device.h"
 #include "kvh_internal.h"
 
@@ -263,6 +265,93 @@ __device__ __forceinline__ void chunk_scores(WaveState<D, NT>& s, const KRegs<D>
   }
 }
 
+// Prefill variant of chunk_scores, built for VALU economy (prefill is MFMA/VALU bound):
+//  * the max is taken over raw scores and the scale c = |scale| log2(e) > 0 is folded into
+//    the exp2 argument (one FMA per score); a sign flip of Q makes c > 0 exact;
+//  * the running shift m only moves when some row's max exceeds it by more than
+//    kRescaleSlack (exp2 domain), so P <= 2^kRescaleSlack and the accumulators are
+//    rescaled rarely (a uniform branch). Numerator and denominator share the shift, so the
+//    result is the softmax whatever shift is used;
+//  * MASKED = false for chunks whose keys every valid row of the wave sees.
+constexpr float kRescaleSlack = 8.f;
+
+template <class E, int D, int NT>
+__device__ __forceinline__ void pf_scores(const WaveState<D, NT>& s, const KRegs<D>& kr, f32x4 st[NT][2]) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile) {
+      f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int cc = 0; cc < D / 32; ++cc) a = E::mfma(kr.k[tile][cc], s.q[t][cc], a);
+      st[t][tile] = a;
+    }
+}
+
+// Causal / absent-page mask of one chunk's scores (-inf where the key is not visible).
+template <int NT>
+__device__ __forceinline__ void pf_mask(f32x4 st[NT][2], const int limit[NT], const ChunkRef& ch) {
+  const int j = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile) {
+      // keys tok < lim are kept: the row's causal limit, or none for an absent page
+      const int lim = ch.blk[tile] >= 0 ? limit[t] - (ch.tok0 + 16 * tile + 4 * j) : INT32_MIN;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st[t][tile][e] = e < lim ? st[t][tile][e] : -INFINITY;
+    }
+}
+
+// Online-softmax update from (masked) raw scores; c > 0 so a -inf score gives P = 0.
+template <class E, int D, int NT>
+__device__ __forceinline__ void pf_softmax(WaveState<D, NT>& s, const f32x4 st[NT][2], float c, u32x4 pt[NT]) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    float mx = fmaxf(fmaxf(fmaxf(st[t][0][0], st[t][0][1]), fmaxf(st[t][0][2], st[t][0][3])),
+                     fmaxf(fmaxf(st[t][1][0], st[t][1][1]), fmaxf(st[t][1][2], st[t][1][3])));
+    mx = max_over_groups(mx);
+    const float ms = mx * c;  // -inf stays -inf (c > 0)
+    if (__builtin_amdgcn_ballot_w64(ms > s.m[t] + kRescaleSlack)) {
+      const float m_new = fmaxf(s.m[t], ms);
+      // the ballot is wave-wide: a row with no visible key so far keeps m = -inf
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(s.m[t] - m_new);
+      s.l[t] *= alpha;
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) s.acc[t][i] *= alpha;
+      s.m[t] = m_new;
+    }
+    const float nshift = s.m[t] == -INFINITY ? 0.f : -s.m[t];
+    float pv[8], psum = 0.f;
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = fast_exp2(__builtin_fmaf(st[t][tile][e], c, nshift));
+        pv[4 * tile + e] = x;
+        psum += x;
+      }
+    s.l[t] += psum;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pt[t][w] = E::pack2(pv[2 * w], pv[2 * w + 1]);
+  }
+}
+
+// Zero the V rows of keys that are absent (blk < 0) or past data_end, like the reference's
+// masked loads (other=0.0), so that stale non-finite values never reach the accumulators.
+template <int D>
+__device__ __forceinline__ void zero_absent_v(VRegs<D>& vr, const ChunkRef& c, int data_end) {
+  constexpr int VW = D / 16;
+  const int j = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int t8 = 0; t8 < 8; ++t8) {
+    const int tok = c.tok0 + 16 * (t8 >> 2) + 4 * j + (t8 & 3);
+    const bool keep = c.blk[t8 >> 2] >= 0 && tok < data_end;
+#pragma unroll
+    for (int x = 0; x < VW / 2; ++x) vr.v[t8][x] = keep ? vr.v[t8][x] : 0u;
+  }
+}
+
 // O^T += V^T P^T for one chunk. In the masked case, slots at or past seq_len may hold any
 // bits (stale or never written cache slots): P is 0 there but 0 * NaN is NaN, so V is
 // zeroed like the reference's masked loads (other=0.0).
@@ -363,6 +452,16 @@ __device__ __forceinline__ SeqView seq_view(const PAParams& p, int seq) {
   const int64_t sl = p.seq_lens[seq];
   v.ctx = sl - v.q_len;
   v.kv_total = (int)clamp64(sl, 0, (int64_t)p.W * p.BS);
+  return v;
+}
+
+// seq_view for a wave-uniform sequence index, with wave-uniform (scalar) results.
+__device__ __forceinline__ SeqView seq_view_uniform(const PAParams& p, int seq) {
+  SeqView v = seq_view(p, seq);
+  v.qs = uni64(v.qs);
+  v.q_len = uni(v.q_len);
+  v.ctx = uni64(v.ctx);
+  v.kv_total = uni(v.kv_total);
   return v;
 }
 
@@ -673,30 +772,95 @@ struct PrefillLds {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// This wave's share of the direct loads of chunk `tok0` into ring stage `stage`.
+// Block ids and in-page offsets of the two 16-token halves of one 32-key chunk (uniform).
+// An id is -1 for a page past the tile's last key, or an id outside the pool.
+struct ChunkIds {
+  int b[2];
+  int off[2];
+};
+
+// Incremental position of a chunk in the paged layout (no division per step).
+struct ChunkPos {
+  int pg, off;  // page and in-page offset of the chunk's first token
+};
+
+__device__ __forceinline__ void chunk_pos_next(ChunkPos& c, int BS) {
+  c.off += kChunk;
+  while (c.off >= BS) {
+    c.off -= BS;
+    ++c.pg;
+  }
+}
+
+// Scalar loads of the chunk's block ids; the table index is clamped so the load is always
+// in the row (W >= 1), and the id is discarded when the page is past page_end. The table
+// is read through the constant address space (it is never written by a kernel): the loads
+// are scalar and counted by lgkmcnt, so waiting for them never waits for the K/V loads in
+// flight (vmcnt is in order).
+typedef const __attribute__((address_space(4))) int64_t* const_i64_ptr;
+
+__device__ __forceinline__ ChunkIds chunk_ids(const PAParams& p, const int64_t* btrow, const ChunkPos& c,
+                                              int page_end) {
+  ChunkIds r;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int o = c.off + 16 * h;
+    const int pg = o >= p.BS ? c.pg + 1 : c.pg;
+    r.off[h] = o >= p.BS ? o - p.BS : o;
+    const int idx = max(0, min(pg, min(page_end, p.W) - 1));
+    const int64_t blk = ((const_i64_ptr)btrow)[idx];
+    r.b[h] = (pg < page_end && blk >= 0 && blk < p.num_blocks) ? (int)blk : -1;
+  }
+  return r;
+}
+
+// One wave's share of the direct global->LDS loads of a chunk: kLoadsPerWave loads of
+// kRowsPerLoad rows each, all of K or all of V and all in the same 16-token half, so one
+// block id and one uniform base address per wave and chunk; the rows and swizzled slots
+// of the loads are folded into per-lane byte offsets.
 template <int D>
-__device__ __forceinline__ void prefill_issue(char* lds, int stage, const PAParams& p, PageWindow& pw,
-                                              const int64_t* btrow, int kvh, int tok0, int page_end, int w) {
+struct PfLoads {
+  using L = PrefillLds<D>;
+  static_assert(L::kLoadsPerWave * L::kRowsPerLoad == 16, "a wave's loads cover one 16-token half");
+  static_assert(L::kLoadsPerTile % L::kLoadsPerWave == 0, "a wave's loads are all K or all V");
+  const char* cache;  // kc or vc
+  int64_t sb, ss;     // block and slot strides of that cache (elements)
+  int h;              // the half (0: tokens 0-15 of the chunk, 1: 16-31)
+  int dst;            // LDS byte offset of the first load within a stage
+  uint32_t loff[L::kLoadsPerWave];
+};
+
+template <int D>
+__device__ __forceinline__ void pf_loads_init(PfLoads<D>& pl, const PAParams& p, int w, int kvh) {
   using L = PrefillLds<D>;
   const int lane = threadIdx.x & 63;
   const int row_in = lane / L::kSlots, slot = lane % L::kSlots;
+  const int g0 = w * L::kLoadsPerWave;
+  const bool v = g0 / L::kLoadsPerTile != 0;
+  const int i0 = g0 % L::kLoadsPerTile;
+  pl.sb = v ? p.v_sb : p.k_sb;
+  pl.ss = v ? p.v_ss : p.k_ss;
+  pl.cache = (const char*)(v ? p.vc : p.kc) + (int64_t)kvh * (v ? p.v_sh : p.k_sh) * 2;
+  pl.h = i0 * L::kRowsPerLoad / 16;
+  pl.dst = (v ? L::kTileBytes : 0) + i0 * 1024;
 #pragma unroll
   for (int k = 0; k < L::kLoadsPerWave; ++k) {
-    const int g = w * L::kLoadsPerWave + k;  // 0 .. 2 * kLoadsPerTile - 1
-    const int which = g / L::kLoadsPerTile;  // 0: K, 1: V
-    const int i = g % L::kLoadsPerTile;
-    const int row0 = i * L::kRowsPerLoad;    // the load's rows share one page (BS % 16 == 0)
-    const int tok = tok0 + row0;
-    int blk = page_block(pw, p, btrow, tok / p.BS, page_end);
-    if (blk < 0) blk = 0;                    // absent page: read block 0, masked later
-    const int row = row0 + row_in;
-    const int64_t sb = which ? p.v_sb : p.k_sb, ss = which ? p.v_ss : p.k_ss, sh = which ? p.v_sh : p.k_sh;
-    const char* base = (const char*)(which ? p.vc : p.kc);
-    const char* src = base + ((int64_t)blk * sb + (int64_t)((tok % p.BS) + row_in) * ss + (int64_t)kvh * sh) * 2 +
-                      16 * (slot ^ (row % L::kSlots));
-    char* dst = lds + stage * L::kStageBytes + which * L::kTileBytes + i * 1024;
-    __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)dst, 16, 0, 0);
+    const int row = (i0 + k) * L::kRowsPerLoad + row_in;  // row of the chunk (0..31)
+    pl.loff[k] = (uint32_t)((row % 16) * pl.ss * 2) + 16u * (uint32_t)(slot ^ (row % L::kSlots));
   }
+}
+
+template <int D>
+__device__ __forceinline__ void pf_issue(char* lds_stage, const PfLoads<D>& pl, const ChunkIds& ids) {
+  using L = PrefillLds<D>;
+  const int b = pl.h ? ids.b[1] : ids.b[0];  // selects, not an indexed load
+  const int off = pl.h ? ids.off[1] : ids.off[0];
+  const int64_t blk = b < 0 ? 0 : b;  // absent page: read block 0, masked later
+  const char* base = pl.cache + (blk * pl.sb + (int64_t)off * pl.ss) * 2;
+#pragma unroll
+  for (int k = 0; k < L::kLoadsPerWave; ++k)
+    __builtin_amdgcn_global_load_lds((const void*)(base + pl.loff[k]), (lds_ptr_t)(lds_stage + pl.dst + k * 1024), 16,
+                                     0, 0);
 }
 
 template <int D>
@@ -754,6 +918,8 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
                                              int64_t slot) {
   constexpr int NT = kPrefillNQT;
   using L = PrefillLds<D>;
+  c_lo = uni(c_lo);
+  c_hi = uni(c_hi);
   const int wg_row0 = t * kPrefillRows;
   const int wg_last = min(wg_row0 + kPrefillRows - 1, R - 1);
   const int kv_lim = (int)clamp64(sv.ctx + wg_last / p.G + 1, 0, sv.kv_total);
@@ -761,21 +927,55 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
   const int my_last = min(row0 + 16 * NT - 1, R - 1);
   const int my_lim = row0 < R ? (int)clamp64(sv.ctx + my_last / p.G + 1, 0, sv.kv_total) : 0;
 
+  // keys below every valid row's causal limit (that of the wave's first row)
+  const int lim_all = row0 < R ? (int)clamp64(sv.ctx + row0 / p.G + 1, 0, sv.kv_total) : 0;
+
   WaveState<D, NT> s;
   load_q<D, NT>(s, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
+  // The exp2 argument is fma(score, c, -m) with c > 0: for a negative scale S c = (-Q) K^T |c|
+  // (a sign flip of Q is exact), for a zero scale every score is 0 = (0 Q) K^T 1.
+  float c = fabsf(p.qk_scale);
+  if (p.qk_scale < 0.f) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int cc = 0; cc < D / 32; ++cc) s.q[t][cc] ^= 0x80008000u;
+  } else if (p.qk_scale == 0.f) {
+    c = 1.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int cc = 0; cc < D / 32; ++cc) s.q[t][cc] = u32x4{0u, 0u, 0u, 0u};
+  }
   const int64_t* btrow = p.bt + (int64_t)seq * p.bt_rs;
   const int page_end = (kv_lim + p.BS - 1) / p.BS;
-  PageWindow pw;
-  load_window(pw, p, btrow, c_lo * kChunk / p.BS, page_end);
+  PfLoads<D> pl;
+  pf_loads_init<D>(pl, p, w, kvh);
+  // block ids of steps i .. i + 3: step i + 2 is issued this iteration, step i + 3's ids are
+  // loaded one iteration before they are needed
+  ChunkPos pos;
+  pos.pg = c_lo * kChunk / p.BS;
+  pos.off = c_lo * kChunk % p.BS;
+  ChunkIds id0 = chunk_ids(p, btrow, pos, page_end);
+  chunk_pos_next(pos, p.BS);
+  ChunkIds id1 = chunk_ids(p, btrow, pos, page_end);
+  chunk_pos_next(pos, p.BS);
+  ChunkIds id2 = chunk_ids(p, btrow, pos, page_end);
 
   // every wave has finished reading the ring (previous tile) before it is refilled
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   const int n = c_hi - c_lo;
-  if (n > 0) prefill_issue<D>(lds, 0, p, pw, btrow, kvh, c_lo * kChunk, page_end, w);
-  if (n > 1) prefill_issue<D>(lds, 1, p, pw, btrow, kvh, (c_lo + 1) * kChunk, page_end, w);
-  for (int i = 0; i < n; ++i) {
+  // this wave's rows see chunks c_lo .. c_lo + n_my - 1 only; it keeps taking part in the
+  // loads and barriers of the rest (two loops, so the accumulators never merge at a join)
+  const int n_my = max(0, min(n, (my_lim + kChunk - 1) / kChunk - c_lo));
+  pf_issue<D>(lds, pl, id0);
+  if (n > 1) pf_issue<D>(lds + L::kStageBytes, pl, id1);
+  // wait for chunk i, then refill the stage chunk i - 1 used with chunk i + 2
+  auto sync_and_issue = [&](int i) {
+    chunk_pos_next(pos, p.BS);
+    const ChunkIds id3 = chunk_ids(p, btrow, pos, page_end);
     __builtin_amdgcn_sched_barrier(0);
     if (i + 1 < n)
       wait_vm<L::kLoadsPerWave>();  // chunk i + 1 may stay in flight
@@ -783,28 +983,55 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
       wait_vm<0>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    if (i + 2 < n)
-      prefill_issue<D>(lds, (i + 2) % L::kStages, p, pw, btrow, kvh, (c_lo + i + 2) * kChunk, page_end, w);
+    if (i + 2 < n) pf_issue<D>(lds + ((i + 2) % L::kStages) * L::kStageBytes, pl, id2);
     __builtin_amdgcn_sched_barrier(0);
-    const int tok0 = (c_lo + i) * kChunk;
-    if (tok0 < my_lim) {
-      const char* st = lds + (i % L::kStages) * L::kStageBytes;
-      ChunkRef cr;
-      cr.tok0 = tok0;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int tt = tok0 + 16 * h;
-        cr.blk[h] = tt < kv_lim ? peek_block(pw, tt / p.BS) : -1;
-      }
-      KRegs<D> kr;
-      VRegs<D> vr;
-      prefill_read_k<D>(kr, st);
-      prefill_read_v<D>(vr, st + L::kTileBytes);
-      u32x4 pt[NT];
-      chunk_scores<E, D, NT, true, false>(s, kr, p, cr, pt);
-      chunk_pv<E, D, NT, true>(s, vr, cr, sv.kv_total, pt);
+    const ChunkIds cur = id0;
+    id0 = id1;
+    id1 = id2;
+    id2 = id3;
+    return cur;
+  };
+  // chunk i with ids idc: MASKED applies the causal limits and absent pages
+  auto compute = [&](int i, const ChunkIds& idc, auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
+    const char* st = lds + (i % L::kStages) * L::kStageBytes;
+    ChunkRef cr;
+    cr.tok0 = (c_lo + i) * kChunk;
+    cr.blk[0] = idc.b[0];
+    cr.blk[1] = idc.b[1];
+    KRegs<D> kr;
+    prefill_read_k<D>(kr, st);
+    f32x4 sc[NT][2];
+    pf_scores<E, D, NT>(s, kr, sc);
+    if (MASKED) pf_mask<NT>(sc, s.limit, cr);
+    u32x4 pt[NT];
+    pf_softmax<E, D, NT>(s, sc, c, pt);
+    VRegs<D> vr;
+    prefill_read_v<D>(vr, st + L::kTileBytes);  // V read late: fewer live registers
+    if (MASKED) zero_absent_v<D>(vr, cr, sv.kv_total);
+    chunk_pv<E, D, NT, false>(s, vr, cr, sv.kv_total, pt);
+  };
+  // Three straight-line loops: chunks every valid row sees whole (no masking), the chunks
+  // on the causal diagonal (masked), then the ones this wave's rows cannot see (loads and
+  // barriers only). An absent page among the first moves to the masked loop.
+  const int n_int = max(0, min(n_my, lim_all / kChunk - c_lo));
+  int i = 0;
+  ChunkIds idc;
+  bool synced = false;
+  for (; i < n_int; ++i) {
+    idc = sync_and_issue(i);
+    if (idc.b[0] < 0 || idc.b[1] < 0) {
+      synced = true;
+      break;
     }
+    compute(i, idc, std::false_type{});
   }
+  for (; i < n_my; ++i) {
+    if (!synced) idc = sync_and_issue(i);
+    synced = false;
+    compute(i, idc, std::true_type{});
+  }
+  for (; i < n; ++i) (void)sync_and_issue(i);
   write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, p.ws_pacc, p.ws_pml, slot * kPrefillRows - wg_row0);
 }
 
@@ -918,7 +1145,7 @@ __global__ __launch_bounds__(256, 2) void pa_prefill_kernel(PAParams p) {
     pre_window(win, p, win.blk0 + 64, win.base + win.total);
   }
   int seq = win.blk0 + li;
-  SeqView sv = seq_view(p, seq);
+  SeqView sv = seq_view_uniform(p, seq);
   int R = sv.q_len * p.G;
   int tiles = (R + kPrefillRows - 1) / kPrefillRows;
   int64_t per_kvh = readlane64(win.c, li) / p.Hkv;
@@ -962,7 +1189,7 @@ __global__ __launch_bounds__(256, 2) void pa_prefill_kernel(PAParams p) {
         }
         li = __builtin_ctzll(nxt);
         seq = win.blk0 + li;
-        sv = seq_view(p, seq);
+        sv = seq_view_uniform(p, seq);
         R = sv.q_len * p.G;
         tiles = (R + kPrefillRows - 1) / kPrefillRows;
         per_kvh = readlane64(win.c, li) / p.Hkv;
