@@ -105,14 +105,14 @@ def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0) -
 
     # per-kernel durations from events the library records around each launch
     lib = _lib.load()
-    ev = HipEvents(4)
+    ev = HipEvents(5)
     per_kernel: dict[str, list[float]] = {}
     HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping)
     for _ in range(prof_iters):
-        lib.kvh_profile_arm(ev.array, 4)
+        lib.kvh_profile_arm(ev.array, 5)
         HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale)
         kinds = last_launch_kernels()
-        for k, kind in enumerate(kinds[:3]):
+        for k, kind in enumerate(kinds[:4]):
             per_kernel.setdefault(kind, []).append(ev.elapsed_ms(k, k + 1))
     ev.close()
     kernel_ms = {k: statistics.mean(v) for k, v in per_kernel.items()}

@@ -129,9 +129,9 @@ KVH_API int kvh_profile_arm(void* const* events, int32_t num_events);
 /* Kernels launched by the last kvh_paged_attention call on this thread, in launch order:
  * writes up to cap kernel-kind codes (KVH_KERNEL_*) and returns how many there were. */
 enum kvh_kernel_kind {
-  KVH_KERNEL_DECODE = 1,   /* split-K decode-class partitions (q_len small) */
-  KVH_KERNEL_PREFILL = 2,  /* prefill/verify-class tiles (q_len large) */
-  KVH_KERNEL_REDUCE = 3,   /* log-sum-exp merge of decode partitions */
+  KVH_KERNEL_DECODE = 1,   /* stream-K decode-class work (q_len small) */
+  KVH_KERNEL_PREFILL = 2,  /* stream-K prefill-class tiles (q_len large) */
+  KVH_KERNEL_REDUCE = 3,   /* log-sum-exp merge of split decode segments and prefill tiles */
   KVH_KERNEL_F32 = 4,      /* exact fp32 path */
 };
 KVH_API int kvh_last_launch_kernels(int32_t* kinds, int32_t cap);

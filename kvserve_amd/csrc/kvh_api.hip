@@ -57,7 +57,8 @@ Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t 
   pl.HGW = Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1);
   pl.slots = (int64_t)B * Hkv / pl.HGW + kMaxDecodeWaves / pl.HGW;
   if (dtype == KVH_DTYPE_F32) {
-    pl.ws_acc_bytes = pl.ws_ml_bytes = pl.ws_job_bytes = pl.ws_pacc_bytes = pl.ws_pml_bytes = pl.ws_bytes = 0;
+    pl.ws_acc_bytes = pl.ws_ml_bytes = pl.ws_job_bytes = pl.ws_pacc_bytes = pl.ws_pml_bytes = pl.ws_plan_bytes =
+        pl.ws_bytes = 0;
   } else {
     const size_t rows = (size_t)pl.slots * pl.HGW * pl.RS;
     pl.ws_acc_bytes = align_up(rows * D * sizeof(float));
@@ -67,7 +68,13 @@ Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t 
     const size_t prows = pl.launch_prefill ? (size_t)2 * kMaxPrefillUnits * kPrefillRows : 0;
     pl.ws_pacc_bytes = align_up(prows * D * sizeof(float));
     pl.ws_pml_bytes = align_up(prows * 2 * sizeof(float));
-    pl.ws_bytes = pl.ws_acc_bytes + pl.ws_ml_bytes + pl.ws_job_bytes + pl.ws_pacc_bytes + pl.ws_pml_bytes;
+    // plan: header, sequence list, flat starts, unit starts
+    pl.ws_plan_bytes = pl.launch_prefill ? align_up(4 * sizeof(int64_t)) + align_up((size_t)B * sizeof(int32_t)) +
+                                               align_up(((size_t)B + 1) * sizeof(int64_t)) +
+                                               align_up((size_t)kMaxPrefillUnits * 4 * sizeof(int32_t))
+                                         : 0;
+    pl.ws_bytes = pl.ws_acc_bytes + pl.ws_ml_bytes + pl.ws_job_bytes + pl.ws_pacc_bytes + pl.ws_pml_bytes +
+                  pl.ws_plan_bytes;
   }
   (void)T;
   return pl;
@@ -242,6 +249,16 @@ int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stri
     p.ws_pacc = plan.ws_pacc_bytes ? (float*)w : nullptr;
     w += plan.ws_pacc_bytes;
     p.ws_pml = plan.ws_pml_bytes ? (float*)w : nullptr;
+    w += plan.ws_pml_bytes;
+    if (plan.ws_plan_bytes) {
+      p.ws_plan_hdr = (int64_t*)w;
+      w += align_up(4 * sizeof(int64_t));
+      p.ws_pre_list = (int32_t*)w;
+      w += align_up((size_t)num_seqs * sizeof(int32_t));
+      p.ws_pre_beg = (int64_t*)w;
+      w += align_up(((size_t)num_seqs + 1) * sizeof(int64_t));
+      p.ws_pre_unit = (int32_t*)w;
+    }
   }
 
   hipStream_t s = (hipStream_t)stream;

@@ -48,6 +48,11 @@ struct PAParams {
   float* ws_pacc;  // [2 kMaxPrefillUnits, kPrefillRows, D] partial outputs of split prefill tiles
   float* ws_pml;   // [2 kMaxPrefillUnits, kPrefillRows, 2]
   int32_t* ws_job; // [kMaxJobs, kJobInts] merge jobs, rewritten by every unit on every call
+  // prefill plan, written by pa_plan_kernel before the prefill launch:
+  int64_t* ws_plan_hdr;  // [4]: flat size C, active units NUa, prefill sequences n_pre
+  int32_t* ws_pre_list;  // [B] the prefill-class sequences in order
+  int64_t* ws_pre_beg;   // [B + 1] flat start of each (ws_pre_beg[n_pre] = C)
+  int32_t* ws_pre_unit;  // [kMaxPrefillUnits, 4] start of unit u: list index, kv head, tile, offset
 };
 
 // Launch plan: a pure function of static shapes (graph-capture safe).
@@ -56,7 +61,7 @@ struct Plan {
   int32_t HGW;              // kv heads per decode work unit
   bool launch_prefill;      // max_query_len > QS
   int64_t slots;            // partial slots: B * Hkv / HGW + kMaxDecodeWaves / HGW
-  size_t ws_acc_bytes, ws_ml_bytes, ws_job_bytes, ws_pacc_bytes, ws_pml_bytes, ws_bytes;
+  size_t ws_acc_bytes, ws_ml_bytes, ws_job_bytes, ws_pacc_bytes, ws_pml_bytes, ws_plan_bytes, ws_bytes;
 };
 
 Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t W, int32_t BS, int32_t max_q,

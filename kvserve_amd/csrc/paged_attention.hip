@@ -444,15 +444,19 @@ struct SeqView {
   int kv_total;  // keys present: seq_len clamped to the block-table capacity
 };
 
-__device__ __forceinline__ SeqView seq_view(const PAParams& p, int seq) {
+// From the raw metadata of a sequence: query_start_loc[s], query_start_loc[s + 1], seq_lens[s].
+__device__ __forceinline__ SeqView seq_view_from(const PAParams& p, int64_t qs_raw, int64_t qe_raw, int64_t sl) {
   SeqView v;
-  v.qs = clamp64(p.qsl[seq], 0, p.T);
-  const int64_t qe = clamp64(p.qsl[seq + 1], v.qs, p.T);
+  v.qs = clamp64(qs_raw, 0, p.T);
+  const int64_t qe = clamp64(qe_raw, v.qs, p.T);
   v.q_len = (int)(qe - v.qs);
-  const int64_t sl = p.seq_lens[seq];
   v.ctx = sl - v.q_len;
   v.kv_total = (int)clamp64(sl, 0, (int64_t)p.W * p.BS);
   return v;
+}
+
+__device__ __forceinline__ SeqView seq_view(const PAParams& p, int seq) {
+  return seq_view_from(p, p.qsl[seq], p.qsl[seq + 1], p.seq_lens[seq]);
 }
 
 // seq_view for a wave-uniform sequence index, with wave-uniform (scalar) results.
@@ -575,13 +579,22 @@ __device__ __forceinline__ int64_t active_units(int64_t C, int NU) {
   return want < 1 ? 1 : (want < NU ? want : NU);
 }
 
+constexpr int kPlanThreads = 256;    // the decode kernel's workgroup
+constexpr int kPlanLdsSeqs = 1024;  // flat starts kept in LDS for the unit search (else global)
+__device__ void plan_prefill(const PAParams& p);
+
 // Decode class: grid (NU * HGW / 4) workgroups of 4 waves; wave w of workgroup b is head
-// w % HGW of unit (4 b + w) / HGW.
+// w % HGW of unit (4 b + w) / HGW. In mixed batches (NUP > 0) workgroup 0 computes the
+// prefill plan instead and the units start at workgroup 1.
 template <class E, int D, int NT>
 __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
+  if (p.NUP > 0 && blockIdx.x == 0) {
+    plan_prefill(p);
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int gw = blockIdx.x * kWavesPerWG + wave;
+  const int gw = (blockIdx.x - (p.NUP > 0 ? 1 : 0)) * kWavesPerWG + wave;
   const int unit = gw / p.HGW, hw = gw % p.HGW;
   const int NHG = p.Hkv / p.HGW;
 
@@ -1043,161 +1056,183 @@ __device__ __forceinline__ int pre_tile_chunks(const PAParams& p, const SeqView&
   return max(1, (lim + kChunk - 1) / kChunk);
 }
 
-// Chunks of all tiles of one kv head of a prefill-class sequence; 0 for other sequences.
+// Fixed cost of a tile (Q load, pipeline fill, output write) in chunk steps: each tile
+// occupies kTileCost + chunks positions of the flat space, the first kTileCost virtual.
+constexpr int kTileCost = 4;
+
+// Flat positions of all tiles of one kv head of a prefill-class sequence; 0 for others.
 __device__ __forceinline__ int64_t pre_seq_chunks(const PAParams& p, const SeqView& sv) {
   if (sv.q_len <= p.QS) return 0;
   const int R = sv.q_len * p.G;
   const int tiles = (R + kPrefillRows - 1) / kPrefillRows;
   int64_t n = 0;
-  for (int t = 0; t < tiles; ++t) n += pre_tile_chunks(p, sv, R, t);
+  for (int t = 0; t < tiles; ++t) n += kTileCost + pre_tile_chunks(p, sv, R, t);
   return n;
 }
 
-__device__ __forceinline__ int64_t readlane64(int64_t x, int l) {
-  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)x, l);
-  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)x >> 32), l);
-  return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-
-// Inclusive prefix sum over the 64 lanes; `total` gets the uniform sum.
-__device__ __forceinline__ int64_t wave_scan64(int64_t x, int64_t& total) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int64_t y = __shfl_up(x, o);
-    if (lane >= o) x += y;
+// Prefill plan, computed by workgroup 0 of the decode launch in mixed batches (so it runs
+// under the decode work instead of ahead of it): the list of prefill-class sequences, the
+// flat start of each (prefix sums of Hkv x pre_seq_chunks) and, for each work unit u < NUa,
+// the sequence (list index), kv head, tile and position within the tile of its first flat
+// position u C / NUa. Every prefill workgroup then starts from two loads instead of
+// scanning the batch itself.
+__device__ void plan_prefill(const PAParams& p) {
+  __shared__ int64_t s_pos[kPlanThreads];
+  __shared__ int32_t s_cnt[kPlanThreads];
+  __shared__ int64_t s_beg[kPlanLdsSeqs + 1];
+  const int tid = threadIdx.x;
+  const int per = (p.B + kPlanThreads - 1) / kPlanThreads;
+  const int s0 = min(tid * per, p.B), s1 = min(s0 + per, p.B);
+  int64_t pos = 0;
+  int cnt = 0;
+  for (int sq = s0; sq < s1; ++sq) {
+    const int64_t c = (int64_t)p.Hkv * pre_seq_chunks(p, seq_view(p, sq));
+    pos += c;
+    cnt += c > 0;
   }
-  total = readlane64(x, 63);
-  return x;
-}
-
-// 64 consecutive sequences of the prefill flat space; lane l describes sequence blk0 + l.
-struct PreWindow {
-  int blk0;
-  int64_t base;   // flat chunks of all sequences before blk0
-  int64_t c;      // this lane's sequence: Hkv x its chunks per kv head
-  int64_t excl;   // flat chunks of sequences blk0 .. blk0 + l - 1
-  int64_t total;  // the whole window
-};
-
-__device__ __forceinline__ void pre_window(PreWindow& w, const PAParams& p, int blk0, int64_t base) {
-  const int s = blk0 + (threadIdx.x & 63);
-  w.blk0 = blk0;
-  w.base = base;
-  w.c = s < p.B ? (int64_t)p.Hkv * pre_seq_chunks(p, seq_view(p, s)) : 0;
-  w.excl = wave_scan64(w.c, w.total) - w.c;
+  s_pos[tid] = pos;
+  s_cnt[tid] = cnt;
+  __syncthreads();
+  for (int o = 1; o < kPlanThreads; o <<= 1) {  // inclusive scan over the threads' ranges
+    const int64_t a = tid >= o ? s_pos[tid - o] : 0;
+    const int b = tid >= o ? s_cnt[tid - o] : 0;
+    __syncthreads();
+    s_pos[tid] += a;
+    s_cnt[tid] += b;
+    __syncthreads();
+  }
+  const int64_t C = s_pos[kPlanThreads - 1];
+  const int n_pre = s_cnt[kPlanThreads - 1];
+  int64_t beg = s_pos[tid] - pos;
+  int k = s_cnt[tid] - cnt;
+  for (int sq = s0; sq < s1; ++sq) {
+    const int64_t c = (int64_t)p.Hkv * pre_seq_chunks(p, seq_view(p, sq));
+    if (c > 0) {
+      p.ws_pre_list[k] = sq;
+      p.ws_pre_beg[k] = beg;
+      if (k < kPlanLdsSeqs) s_beg[k] = beg;
+      beg += c;
+      ++k;
+    }
+  }
+  const int NUa = C > 0 ? (int)active_units(C, p.NUP) : 0;
+  if (tid == 0) {
+    p.ws_plan_hdr[0] = C;
+    p.ws_plan_hdr[1] = NUa;
+    p.ws_plan_hdr[2] = n_pre;
+    p.ws_pre_beg[n_pre] = C;
+    if (n_pre <= kPlanLdsSeqs) s_beg[n_pre] = C;
+  }
+  __syncthreads();  // the list and starts are visible to the whole workgroup
+  const int64_t* beg_tab = n_pre <= kPlanLdsSeqs ? s_beg : p.ws_pre_beg;
+  for (int u = tid; u < NUa; u += kPlanThreads) {
+    const int64_t x0 = u * C / NUa;
+    int lo = 0, hi = n_pre - 1;  // last sequence starting at or before x0
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) / 2;
+      if (beg_tab[mid] <= x0)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const SeqView sv = seq_view(p, p.ws_pre_list[lo]);
+    const int R = sv.q_len * p.G;
+    const int64_t per_kvh = (beg_tab[lo + 1] - beg_tab[lo]) / p.Hkv;
+    const int64_t off = x0 - beg_tab[lo];
+    const int kvh = (int)(off / per_kvh);
+    int64_t rem = off % per_kvh;
+    int t = 0;
+    for (int n_t = pre_tile_chunks(p, sv, R, 0); rem >= kTileCost + n_t; n_t = pre_tile_chunks(p, sv, R, t)) {
+      rem -= kTileCost + n_t;
+      ++t;
+    }
+    int32_t* d = p.ws_pre_unit + (int64_t)u * 4;
+    d[0] = lo;
+    d[1] = kvh;
+    d[2] = t;
+    d[3] = (int)rem;  // < kTileCost + chunks of one tile
+  }
 }
 
 // Stream-K over the prefill-class work: a flat space of (sequence, kv head, tile, chunk),
-// sequence-major, in which tile t of (seq, kvh) contributes pre_tile_chunks chunks. The
-// launch has one workgroup per resident slot (NUP, a multiple of 8); NUa = min(NUP,
-// ceil(C / kMinUnitChunks)) of them are work units, unit u taking chunks [u C / NUa,
-// (u + 1) C / NUa), so every unit does the same number of chunk steps whatever the mix of
-// prompt lengths, and none is empty. A tile split between units leaves partials: unit u
-// keeps the piece of its first tile in slot 2u and of its last tile in slot 2u + 1 (tiles
-// in between are whole and written out), and the unit holding a split tile's first piece
-// records its merge job (in the record of its workgroup). Workgroups are dealt to the 8
-// XCDs round-robin, so the units are numbered XCD by XCD: the units of one XCD are
-// contiguous in the flat space and read the same sequence's K/V through that XCD's L2.
+// sequence-major, in which tile t of (seq, kvh) occupies kTileCost + pre_tile_chunks
+// positions (its fixed cost counted like chunk steps). The launch has one workgroup per
+// resident slot (NUP, a multiple of 8); NUa = min(NUP, ceil(C / kMinUnitChunks)) of them are
+// work units, unit u taking positions [u C / NUa, (u + 1) C / NUa), so every unit gets the
+// same amount of work whatever the mix of prompt lengths. A tile split between units leaves
+// partials: unit u keeps the piece of its first non-empty tile in slot 2u and of its last in
+// slot 2u + 1 (tiles in between are whole and written out), and the unit holding a split
+// tile's first piece records its merge job (in the record of its workgroup). Workgroups are
+// dealt to the 8 XCDs round-robin, so the units are numbered XCD by XCD: the units of one
+// XCD are contiguous in the flat space and read the same sequence's K/V through that
+// XCD's L2.
 template <class E, int D>
 __global__ __launch_bounds__(256, 2) void pa_prefill_kernel(PAParams p) {
   using L = PrefillLds<D>;
   __shared__ __attribute__((aligned(1024))) char lds[L::kStages * L::kStageBytes];
-  const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int32_t* job = p.ws_job + (int64_t)(kMaxDecodeWaves + blockIdx.x) * kJobInts;
   if (threadIdx.x == 0) job[0] = kJobNone;
 
-  // Flat size C: lane l sums the sequences l K .. l K + K - 1, then one wave scan.
-  const int K = (p.B + 63) / 64;
-  int64_t mine = 0;
-  for (int i = 0; i < K; ++i) {
-    const int sq = lane * K + i;
-    if (sq < p.B) mine += (int64_t)p.Hkv * pre_seq_chunks(p, seq_view(p, sq));
-  }
-  int64_t C;
-  const int64_t incl = wave_scan64(mine, C);
-  if (C == 0) return;
-  const int NUa = (int)active_units(C, p.NUP);
+  const int64_t C = uni64(p.ws_plan_hdr[0]);
+  const int NUa = (int)uni64(p.ws_plan_hdr[1]);
+  const int n_pre = (int)uni64(p.ws_plan_hdr[2]);
+  if (C == 0 || NUa <= 0) return;
   const int xcd = (int)(blockIdx.x % 8), j = (int)(blockIdx.x / 8);
   const int q8 = NUa / 8, r8 = NUa % 8;
   if (j >= q8 + (xcd < r8 ? 1 : 0)) return;  // idle workgroup (workgroup-uniform)
   const int u = xcd * q8 + min(xcd, r8) + j;
-  const int64_t x0 = u * C / NUa, x1 = (u + 1) * C / NUa;
-  if (x0 >= x1) return;  // cannot happen: NUa <= C
+  int64_t x = u * C / NUa;
+  const int64_t x1 = (u + 1) * C / NUa;
 
-  // The window of 64 sequences from the block holding x0, then the sequence itself.
-  const uint64_t blk_hit = __builtin_amdgcn_ballot_w64(mine > 0 && incl - mine <= x0 && x0 < incl);
-  if (blk_hit == 0) return;  // cannot happen for consistent metadata
-  const int lb = __builtin_ctzll(blk_hit);
-  PreWindow win;
-  pre_window(win, p, lb * K, readlane64(incl - mine, lb));
-  int64_t x = x0;
-  int li = -1;
-  for (;;) {
-    const uint64_t hit = __builtin_amdgcn_ballot_w64(win.c > 0 && win.base + win.excl <= x &&
-                                                     x < win.base + win.excl + win.c);
-    if (hit) {
-      li = __builtin_ctzll(hit);
-      break;
-    }
-    if (win.blk0 + 64 >= p.B) return;  // cannot happen for consistent metadata
-    pre_window(win, p, win.blk0 + 64, win.base + win.total);
-  }
-  int seq = win.blk0 + li;
+  const int32_t* ud = p.ws_pre_unit + (int64_t)u * 4;
+  int k = uni(ud[0]);
+  int kvh = uni(ud[1]);
+  int t = uni(ud[2]);
+  int seq = uni(p.ws_pre_list[k]);
   SeqView sv = seq_view_uniform(p, seq);
   int R = sv.q_len * p.G;
   int tiles = (R + kPrefillRows - 1) / kPrefillRows;
-  int64_t per_kvh = readlane64(win.c, li) / p.Hkv;
-  const int64_t off = x - (win.base + readlane64(win.excl, li));
-  int kvh = (int)(off / per_kvh);
-  int64_t rem = off % per_kvh;
-  int t = 0;
-  int n_t = pre_tile_chunks(p, sv, R, 0);
-  while (rem >= n_t) {
-    rem -= n_t;
-    ++t;
-    n_t = pre_tile_chunks(p, sv, R, t);
-  }
-  int c_lo = (int)rem;
+  int n_t = pre_tile_chunks(p, sv, R, t);
+  int64_t rem = uni(ud[3]);
+  // a: this unit's first position within the tile. Positions a .. b - 1 of a tile are its
+  // chunks max(0, a - kTileCost) .. max(0, b - kTileCost) - 1, the same map at both ends
+  // of every unit, so the pieces partition the chunks; a range inside the virtual prefix is
+  // empty and skipped.
+  int64_t a = rem;
   bool first = true;
   for (;;) {
-    const int c_hi = (int)min((int64_t)n_t, c_lo + (x1 - x));
-    const bool whole = c_lo == 0 && c_hi == n_t;
-    const int64_t slot = 2 * (int64_t)u + (first ? 0 : 1);
-    prefill_tile<E, D>(lds, p, sv, R, seq, kvh, t, c_lo, c_hi, w, !whole, slot);
-    if (threadIdx.x == 0 && c_lo == 0 && c_hi < n_t) {
-      // the tile continues in units u + 1 .. u1, each holding it as its first tile
-      const int64_t x_last = x + (n_t - c_lo) - 1;
-      const int64_t u1 = ((x_last + 1) * NUa - 1) / C;
-      write_job(job, kJobPrefill, (int)(u1 - u + 1), slot, 2 * (int64_t)u, 2, sv.qs, R, t * kPrefillRows, kvh);
+    const int64_t tw = kTileCost + n_t;
+    const int64_t b = min(tw, a + (x1 - x));
+    const int c_lo = (int)max((int64_t)0, a - kTileCost), c_hi = (int)max((int64_t)0, b - kTileCost);
+    if (c_hi > c_lo) {
+      const bool whole = c_lo == 0 && c_hi == n_t;
+      const int64_t slot = 2 * (int64_t)u + (first ? 0 : 1);
+      prefill_tile<E, D>(lds, p, sv, R, seq, kvh, t, c_lo, c_hi, w, !whole, slot);
+      if (threadIdx.x == 0 && c_lo == 0 && c_hi < n_t) {
+        // the tile continues in units u + 1 .. u1, each holding it as its first piece
+        const int64_t x_last = x + (tw - a) - 1;
+        const int64_t u1 = ((x_last + 1) * NUa - 1) / C;
+        write_job(job, kJobPrefill, (int)(u1 - u + 1), slot, 2 * (int64_t)u, 2, sv.qs, R, t * kPrefillRows, kvh);
+      }
+      first = false;
     }
-    x += c_hi - c_lo;
+    x += b - a;
     if (x >= x1) break;
-    first = false;
-    c_lo = 0;
+    a = 0;
     if (++t == tiles) {
       t = 0;
       if (++kvh == p.Hkv) {
         kvh = 0;
-        // next sequence with prefill work
-        uint64_t nxt = __builtin_amdgcn_ballot_w64(win.c > 0) & (li < 63 ? ~0ull << (li + 1) : 0ull);
-        while (nxt == 0) {
-          if (win.blk0 + 64 >= p.B) return;  // cannot happen for consistent metadata
-          pre_window(win, p, win.blk0 + 64, win.base + win.total);
-          nxt = __builtin_amdgcn_ballot_w64(win.c > 0);
-        }
-        li = __builtin_ctzll(nxt);
-        seq = win.blk0 + li;
+        if (++k >= n_pre) return;  // cannot happen: the flat space ends with the last sequence
+        seq = uni(p.ws_pre_list[k]);
         sv = seq_view_uniform(p, seq);
         R = sv.q_len * p.G;
         tiles = (R + kPrefillRows - 1) / kPrefillRows;
-        per_kvh = readlane64(win.c, li) / p.Hkv;
       }
     }
     n_t = pre_tile_chunks(p, sv, R, t);
   }
-  (void)per_kvh;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1226,11 +1261,13 @@ static int resident_blocks(const void* kernel) {
 template <class E, int D, int NT>
 static int launch_decode_nt(PAParams& p, hipStream_t s) {
   const void* k = (const void*)&pa_decode_kernel<E, D, NT>;
-  int waves = resident_blocks(k) * kWavesPerWG;
+  const int plan_wgs = p.NUP > 0 ? 1 : 0;  // workgroup 0 plans the prefill launch
+  int waves = (resident_blocks(k) - plan_wgs) * kWavesPerWG;
   if (waves > kMaxDecodeWaves) waves = kMaxDecodeWaves;
+  if (waves < kWavesPerWG) waves = kWavesPerWG;
   p.NU = waves / p.HGW;
   const int wgs = (p.NU * p.HGW + kWavesPerWG - 1) / kWavesPerWG;
-  hipLaunchKernelGGL((pa_decode_kernel<E, D, NT>), dim3(wgs), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((pa_decode_kernel<E, D, NT>), dim3(wgs + plan_wgs), dim3(256), 0, s, p);
   return (int)hipGetLastError();
 }
 
