@@ -337,21 +337,6 @@ __device__ __forceinline__ void pf_softmax(WaveState<D, NT>& s, const f32x4 st[N
   }
 }
 
-// Zero the V rows of keys that are absent (blk < 0) or past data_end, like the reference's
-// masked loads (other=0.0), so that stale non-finite values never reach the accumulators.
-template <int D>
-__device__ __forceinline__ void zero_absent_v(VRegs<D>& vr, const ChunkRef& c, int data_end) {
-  constexpr int VW = D / 16;
-  const int j = (threadIdx.x & 63) >> 4;
-#pragma unroll
-  for (int t8 = 0; t8 < 8; ++t8) {
-    const int tok = c.tok0 + 16 * (t8 >> 2) + 4 * j + (t8 & 3);
-    const bool keep = c.blk[t8 >> 2] >= 0 && tok < data_end;
-#pragma unroll
-    for (int x = 0; x < VW / 2; ++x) vr.v[t8][x] = keep ? vr.v[t8][x] : 0u;
-  }
-}
-
 // O^T += V^T P^T for one chunk. In the masked case, slots at or past seq_len may hold any
 // bits (stale or never written cache slots): P is 0 there but 0 * NaN is NaN, so V is
 // zeroed like the reference's masked loads (other=0.0).
@@ -856,10 +841,23 @@ __device__ __forceinline__ void pf_loads_init(PfLoads<D>& pl, const PAParams& p,
   pl.cache = (const char*)(v ? p.vc : p.kc) + (int64_t)kvh * (v ? p.v_sh : p.k_sh) * 2;
   pl.h = i0 * L::kRowsPerLoad / 16;
   pl.dst = (v ? L::kTileBytes : 0) + i0 * 1024;
+  if (!v) {
 #pragma unroll
-  for (int k = 0; k < L::kLoadsPerWave; ++k) {
-    const int row = (i0 + k) * L::kRowsPerLoad + row_in;  // row of the chunk (0..31)
-    pl.loff[k] = (uint32_t)((row % 16) * pl.ss * 2) + 16u * (uint32_t)(slot ^ (row % L::kSlots));
+    for (int k = 0; k < L::kLoadsPerWave; ++k) {
+      const int row = (i0 + k) * L::kRowsPerLoad + row_in;  // row of the chunk (0..31)
+      pl.loff[k] = (uint32_t)((row % 16) * pl.ss * 2) + 16u * (uint32_t)(slot ^ (row % L::kSlots));
+    }
+  } else {
+    // V stage layout: blocks b = h (D/16) + i of 512 bytes, block b holding d = 16i .. 16i+15
+    // of the 16 tokens of half h, token-major (32 bytes per token). 16-byte granule P of the
+    // stage is token (P % 32) / 2 of the half, global 16-byte chunk 2 (b % (D/16)) + P % 2.
+    pl.h = 2 * i0 / (D / 16);
+#pragma unroll
+    for (int k = 0; k < L::kLoadsPerWave; ++k) {
+      const int P = 64 * (i0 + k) + lane;
+      const int b = P / 32, tok = (P % 32) / 2, chunk = 2 * (b % (D / 16)) + P % 2;
+      pl.loff[k] = (uint32_t)(tok * pl.ss * 2) + 16u * (uint32_t)chunk;
+    }
   }
 }
 
@@ -892,27 +890,75 @@ __device__ __forceinline__ void prefill_read_k(KRegs<D>& r, const char* tile) {
   }
 }
 
-template <int D>
-__device__ __forceinline__ void prefill_read_v(VRegs<D>& r, const char* tile) {
-  using L = PrefillLds<D>;
-  constexpr int VW = D / 16;  // elements per lane per token: d = VW m ..
+// O^T += V^T P^T from the V stage with gfx950 transpose reads. ds_read_b64_tr_b16 hands lane
+// 4q + r of each 16-lane group element r of the 8 bytes read by lanes 4k + q (k = 0..3). With
+// lane l reading block b at byte 8 l, group j (lanes 16j ..) reads tokens 4j .. 4j + 3 of the
+// half, and lane (j, n) receives V[token 4j + k][16i + n] for k = 0..3: the A-operand slots of
+// output tile i in the same token order as P^T (tokens 4j + e of half 0, then of half 1).
+// The accumulator row 4j + e of tile i is then d = 16i + 4j + e. MASKED zeroes the V of
+// tokens that are absent or at/after data_end (other=0.0 in the reference's masked loads).
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4* lds_i16x4_ptr;
+
+template <class E, int D, int NT, bool MASKED>
+__device__ __forceinline__ void pf_pv(WaveState<D, NT>& s, const char* vtile, const ChunkRef& c, int data_end,
+                                      const u32x4 pt[NT]) {
   const int lane = threadIdx.x & 63;
-  const int j = lane >> 4, m = lane & 15;
+  const int j = lane >> 4;
+  uint32_t keep[4] = {~0u, ~0u, ~0u, ~0u};  // dword w: tokens of slots 2w, 2w + 1
+  if (MASKED) {
 #pragma unroll
-  for (int t8 = 0; t8 < 8; ++t8) {
-    const int row = 16 * (t8 >> 2) + 4 * j + (t8 & 3);
-    const int byte = VW * m * 2;  // within the global row
-    const char* src = tile + row * L::kRowBytes + 16 * ((byte / 16) ^ (row % L::kSlots)) + byte % 16;
-    if constexpr (VW == 8) {
-      const u32x4 x = *(const u32x4*)src;
-      r.v[t8][0] = x[0];
-      r.v[t8][1] = x[1];
-      r.v[t8][2] = x[2];
-      r.v[t8][3] = x[3];
+    for (int w = 0; w < 4; ++w) {
+      const int h = w >> 1;
+      const int tok = c.tok0 + 16 * h + 4 * j + 2 * (w & 1);
+      const bool ok = c.blk[h] >= 0;
+      keep[w] = (ok && tok < data_end ? 0x0000ffffu : 0u) | (ok && tok + 1 < data_end ? 0xffff0000u : 0u);
+    }
+  }
+  const __attribute__((address_space(3))) char* base = (const __attribute__((address_space(3))) char*)vtile + 8 * lane;
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) {
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_ptr)(base + 512 * i));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_ptr)(base + 512 * (D / 16 + i)));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+    u32x4 va = {l2[0], l2[1], h2[0], h2[1]};
+    if (MASKED) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) va[w] &= keep[w];
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) s.acc[t][i] = E::mfma(va, pt[t], s.acc[t][i]);
+  }
+}
+
+// Prefill output / partial rows from the pf_pv accumulator layout (d = 16i + 4j + e).
+template <class E, int D, int NT>
+__device__ __forceinline__ void pf_write_rows(const WaveState<D, NT>& s, const PAParams& p, const SeqView& sv,
+                                              int R, int row0, int kvh, bool partial, int64_t row_base) {
+  const int lane = threadIdx.x & 63;
+  const int j = lane >> 4, n = lane & 15;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const float L = sum_over_groups(s.l[t]);
+    const int r = row0 + 16 * t + n;
+    if (r >= R) continue;
+    if (!partial) {
+      const int qi = r / p.G, g = r % p.G;
+      const float inv = 1.f / (L == 0.f ? 1.f : L);
+      uint16_t* base = (uint16_t*)p.out + (sv.qs + qi) * p.o_ts + (int64_t)(kvh * p.G + g) * p.o_hs + 4 * j;
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i)
+        *(u32x2*)(base + 16 * i) = u32x2{E::pack2(s.acc[t][i][0] * inv, s.acc[t][i][1] * inv),
+                                         E::pack2(s.acc[t][i][2] * inv, s.acc[t][i][3] * inv)};
     } else {
-      const u32x2 x = *(const u32x2*)src;
-      r.v[t8][0] = x[0];
-      r.v[t8][1] = x[1];
+      const int64_t idx = row_base + r;
+      float* dst = p.ws_pacc + idx * D + 4 * j;
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) *(f32x4*)(dst + 16 * i) = s.acc[t][i];
+      if (j == 0) {
+        p.ws_pml[idx * 2] = s.m[t];
+        p.ws_pml[idx * 2 + 1] = L;
+      }
     }
   }
 }
@@ -1019,10 +1065,7 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
     if (MASKED) pf_mask<NT>(sc, s.limit, cr);
     u32x4 pt[NT];
     pf_softmax<E, D, NT>(s, sc, c, pt);
-    VRegs<D> vr;
-    prefill_read_v<D>(vr, st + L::kTileBytes);  // V read late: fewer live registers
-    if (MASKED) zero_absent_v<D>(vr, cr, sv.kv_total);
-    chunk_pv<E, D, NT, false>(s, vr, cr, sv.kv_total, pt);
+    pf_pv<E, D, NT, MASKED>(s, st + L::kTileBytes, cr, sv.kv_total, pt);
   };
   // Three straight-line loops: chunks every valid row sees whole (no masking), the chunks
   // on the causal diagonal (masked), then the ones this wave's rows cannot see (loads and
@@ -1045,7 +1088,7 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
     compute(i, idc, std::true_type{});
   }
   for (; i < n; ++i) (void)sync_and_issue(i);
-  write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, p.ws_pacc, p.ws_pml, slot * kPrefillRows - wg_row0);
+  pf_write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, slot * kPrefillRows - wg_row0);
 }
 
 // Chunks of tile t (rows 128 t .. of R): those its last row can see, at least one so that
