@@ -10,8 +10,8 @@ namespace kvh {
 // Upper bound on the waves one decode launch uses (256 CUs x 8 waves per SIMD x 4 SIMDs
 // would be 8192); the workspace is sized for it, so its size never depends on the device.
 constexpr int32_t kMaxDecodeWaves = 8192;
-// Upper bound on the workgroups (work units) of one prefill launch: 256 CUs x 2 resident.
-constexpr int32_t kMaxPrefillUnits = 512;
+// Upper bound on the workgroups (work units) of one prefill launch: 256 CUs x 3 resident.
+constexpr int32_t kMaxPrefillUnits = 768;
 // Query rows ((token, head) pairs of one kv head) one prefill workgroup owns.
 constexpr int32_t kPrefillRows = 128;
 // Merge job record: int32 fields, one record per work unit (decode units first).

@@ -1210,7 +1210,7 @@ __device__ void plan_prefill(const PAParams& p) {
 // XCD are contiguous in the flat space and read the same sequence's K/V through that
 // XCD's L2.
 template <class E, int D>
-__global__ __launch_bounds__(256, 2) void pa_prefill_kernel(PAParams p) {
+__global__ __launch_bounds__(256, 3) void pa_prefill_kernel(PAParams p) {
   using L = PrefillLds<D>;
   __shared__ __attribute__((aligned(1024))) char lds[L::kStages * L::kStageBytes];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
