@@ -54,7 +54,7 @@ Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t 
   }
   pl.NT = (pl.QS * G + 15) / 16;
   pl.RS = pl.QS * G;
-  pl.HGW = Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1);
+  pl.HGW = Hkv % 8 == 0 ? 8 : (Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1));
   pl.slots = (int64_t)B * Hkv / pl.HGW + kMaxDecodeWaves / pl.HGW;
   if (dtype == KVH_DTYPE_F32) {
     pl.ws_acc_bytes = pl.ws_ml_bytes = pl.ws_job_bytes = pl.ws_pacc_bytes = pl.ws_pml_bytes = pl.ws_plan_bytes =

@@ -40,7 +40,7 @@ struct PAParams {
   float qk_scale;  // scale * log2(e): scores are kept in the exp2 domain
   int32_t QS;      // sequences with 0 < q_len <= QS are decode class (stream-K kernel)
   int32_t RS;      // query rows of a decode-class sequence at most: QS * G
-  int32_t HGW;     // kv heads (waves) per work unit of the decode kernel: 4, 2 or 1
+  int32_t HGW;     // kv heads (waves) per work unit of the decode kernel: 8, 4, 2 or 1
   int32_t NU;      // work units the decode launch provides (waves / HGW)
   int32_t NUP;     // work units (workgroups) of the prefill launch, 0 when none
   float* ws_acc;   // [slots, HGW, RS, D] unnormalised partial outputs of split decode segments

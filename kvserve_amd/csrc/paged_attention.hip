@@ -22,14 +22,16 @@
 //    second register buffer.
 //  * Decode class (q_len <= QS): stream-K. The launch keeps exactly as many waves as the GPU
 //    holds resident; the decode work of all sequences is one flat space of 32-token chunks
-//    that is cut into equal contiguous ranges, one per work unit of up to 4 waves (adjacent
-//    kv heads of the same rows). No wave idles in a tail and each pays one start-up; a
-//    sequence split between units leaves partials that the reduce kernel merges with a
-//    log-sum-exp. The split is computed on the device from seq_lens (no host sync).
-//  * Prefill class (q_len > QS): a workgroup of 4 waves owns 4 x 32 query rows; each
-//    wave streams every key its rows can see (causal limit of its last row).
-// Grids depend only on static shapes (block-table width, max_query_len), never on
-// per-step lengths, so every launch is HIP-graph capturable.
+//    that is cut into equal contiguous ranges, one per work unit of up to 8 waves (adjacent
+//    kv heads of the same rows: a token's 8 heads are one contiguous 2 KB row at D = 128).
+//    No wave idles in a tail and each pays one start-up; a sequence split between units
+//    leaves partials that the merge kernel combines with a log-sum-exp. The split is
+//    computed on the device from seq_lens (no host sync).
+//  * Prefill class (q_len > QS): stream-K as well, over (sequence, kv head, 128-row tile,
+//    chunk); a workgroup of 4 waves shares each K/V chunk through an LDS ring filled by
+//    direct global->LDS loads, each wave computing 32 query rows.
+// Grids depend only on static shapes and the device's occupancy, never on per-step
+// lengths, so every launch is HIP-graph capturable.
 #include <type_traits>
 
 #include "kvh_device.h"
@@ -84,7 +86,8 @@ __device__ __forceinline__ int peek_block(const PageWindow& pw, int page) {
 // Per-lane registers of one 32-token chunk of one kv head.
 template <int D>
 struct KRegs {
-  u32x4 k[2][D / 32];  // tile t, 8-element vector c: token 16t + n, d = (D/4) j + 8c ..
+  u32x4 k[2][D / 32];  // tile t, 8-element vector c: token 16t + n, d = 32c + 8j ..
+                       // (one load instruction per c reads 64 contiguous bytes of each row)
 };
 template <int D>
 struct VRegs {
@@ -112,7 +115,7 @@ __device__ __forceinline__ ChunkRef chunk_ref(PageWindow& pw, const PAParams& p,
 
 // Lane byte offsets inside a (block, kv head) page, fixed for the whole kernel.
 struct LaneOffsets {
-  uint32_t k;  // (n * k_ss + (D/4) j) * 2
+  uint32_t k;  // (n * k_ss + 8 j) * 2
   uint32_t v;  // (4j * v_ss + VW n) * 2
 };
 
@@ -121,7 +124,7 @@ __device__ __forceinline__ LaneOffsets lane_offsets(const PAParams& p) {
   const int lane = threadIdx.x & 63;
   const int j = lane >> 4, n = lane & 15;
   LaneOffsets o;
-  o.k = (uint32_t)(n * (uint32_t)p.k_ss + (D / 4) * j) * 2u;
+  o.k = (uint32_t)(n * (uint32_t)p.k_ss + 8 * j) * 2u;
   o.v = (uint32_t)(4 * j * (uint32_t)p.v_ss + (D / 16) * n) * 2u;
   return o;
 }
@@ -137,7 +140,7 @@ __device__ __forceinline__ void load_k(KRegs<D>& r, const PAParams& p, const Chu
     const int slot0 = (c.tok0 + 16 * t) % p.BS;
     const char* page = (const char*)p.kc + (blk * p.k_sb + (int64_t)kvh * p.k_sh + (int64_t)slot0 * p.k_ss) * 2;
 #pragma unroll
-    for (int cc = 0; cc < D / 32; ++cc) r.k[t][cc] = *(const u32x4*)(page + k_lane + 16 * cc);
+    for (int cc = 0; cc < D / 32; ++cc) r.k[t][cc] = *(const u32x4*)(page + k_lane + 64 * cc);
   }
 }
 
@@ -192,9 +195,9 @@ __device__ __forceinline__ void load_q(WaveState<D, NT>& s, const PAParams& p, i
     for (int i = 0; i < D / 16; ++i) s.acc[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (r < R) {
       const int qi = r / p.G, g = r % p.G;
-      const uint16_t* qp = q + (q_start + qi) * p.q_ts + (int64_t)(kvh * p.G + g) * p.q_hs + (D / 4) * j;
+      const uint16_t* qp = q + (q_start + qi) * p.q_ts + (int64_t)(kvh * p.G + g) * p.q_hs + 8 * j;
 #pragma unroll
-      for (int c = 0; c < D / 32; ++c) s.q[t][c] = *(const u32x4*)(qp + 8 * c);
+      for (int c = 0; c < D / 32; ++c) s.q[t][c] = *(const u32x4*)(qp + 32 * c);
       s.limit[t] = (int)clamp64(ctx + qi + 1, 0, kv_total);
     } else {
 #pragma unroll
@@ -884,7 +887,7 @@ __device__ __forceinline__ void prefill_read_k(KRegs<D>& r, const char* tile) {
     const int row = 16 * t + n;
 #pragma unroll
     for (int cc = 0; cc < D / 32; ++cc) {
-      const int gslot = (D / 32) * j + cc;  // global 16-byte slot: d = (D/4) j + 8 cc
+      const int gslot = 4 * cc + j;  // global 16-byte slot: d = 32 cc + 8 j
       r.k[t][cc] = *(const u32x4*)(tile + row * L::kRowBytes + 16 * (gslot ^ (row % L::kSlots)));
     }
   }

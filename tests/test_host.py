@@ -109,13 +109,13 @@ def test_cache_write_validation(lib):
 
 def test_workspace_follows_the_plan(lib):
     """Decode partial slots: one per (sequence, head group) plus one per possible decode work
-    unit (8192 waves / 4 heads per unit), each holding RS = QS * G rows; merge-job records
+    unit (8192 waves / 8 heads per unit when Hkv % 8 == 0), each holding RS = QS * G rows; merge-job records
     (16 int32) for 8192 decode units, plus 768 prefill units, their two 128-row partial
     slots each and the prefill plan (sequence list, flat starts, unit starts) when the batch
     has prefill-class queries."""
     ws = lib.kvh_paged_attention_workspace_size
 
-    def want(B, Hkv, G, QS, D, hgw=4, prefill=False):
+    def want(B, Hkv, G, QS, D, hgw=8, prefill=False):
         slots = B * Hkv // hgw + 8192 // hgw
         rows = slots * hgw * QS * G
         up = lambda x: -(-x // 256) * 256  # noqa: E731
