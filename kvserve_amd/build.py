@@ -24,6 +24,11 @@ INCLUDE = PKG.parent / "include"
 
 SOURCES = ["kvh_api.hip", "paged_attention.hip", "paged_attention_f32.hip", "reshape_and_cache.hip"]
 
+# Per-source additions. The MFMA kernels treat scores as finite (masked keys become -inf by
+# selects, never by arithmetic on NaN), so fmaxf needs no sNaN canonicalisation: without
+# -fno-honor-nans every max of an MFMA result costs an extra v_max_f32 x, x, x.
+SOURCE_FLAGS = {"paged_attention.hip": ["-fno-honor-nans"]}
+
 # -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32 (unreliable on these
 # hosts); the host pass warns that it does not know the feature, which is harmless.
 HIP_FLAGS = [
@@ -78,7 +83,7 @@ def build(
 
     def compile_one(src: str) -> Path:
         obj = objdir / (Path(src).stem + ".o")
-        cmd = [cc, *flags, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *flags, *SOURCE_FLAGS.get(src, []), f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd))
         _run(cmd)

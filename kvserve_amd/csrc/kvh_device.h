@@ -36,6 +36,12 @@ struct BF16 {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
   }
   static __device__ __forceinline__ float to_f32(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
+  // acc + lo + hi of a packed pair (v_dot2_f32_bf16 against {1, 1})
+  static __device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x), __builtin_bit_cast(bf16x2_t, 0x3f803f80u),
+                                           acc, false);
+  }
 };
 
 struct F16 {
@@ -51,6 +57,11 @@ struct F16 {
   }
   static __device__ __forceinline__ float to_f32(uint16_t x) {
     return (float)__builtin_bit_cast(_Float16, x);
+  }
+  // acc + lo + hi of a packed pair (v_dot2_f32_f16 against {1, 1})
+  static __device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), __builtin_bit_cast(f16x2_t, 0x3c003c00u), acc, false);
   }
 };
 

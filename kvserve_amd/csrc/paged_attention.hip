@@ -177,6 +177,7 @@ struct WaveState {
   f32x4 acc[NT][D / 16];  // O^T accumulators: column = row, rows 4j+e <-> d = VW*(4j+e) + i
   float m[NT], l[NT];     // m: running max (exp2 domain, -inf when empty); l: lane-partial sum
   int limit[NT];          // keys visible to this lane's row (0 for padding rows)
+  float thr[NT], nsh[NT]; // prefill only: raw-score bound that moves m, and -m (0 while m = -inf)
 };
 
 // Q rows of tile t: global row r = row0 + 16t + n, valid when r < R.
@@ -191,6 +192,8 @@ __device__ __forceinline__ void load_q(WaveState<D, NT>& s, const PAParams& p, i
     const int r = row0 + 16 * t + n;
     s.m[t] = -INFINITY;
     s.l[t] = 0.f;
+    s.thr[t] = -INFINITY;
+    s.nsh[t] = 0.f;
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) s.acc[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (r < R) {
@@ -306,37 +309,49 @@ __device__ __forceinline__ void pf_mask(f32x4 st[NT][2], const int limit[NT], co
     }
 }
 
-// Online-softmax update from (masked) raw scores; c > 0 so a -inf score gives P = 0.
-template <class E, int D, int NT>
-__device__ __forceinline__ void pf_softmax(WaveState<D, NT>& s, const f32x4 st[NT][2], float c, u32x4 pt[NT]) {
+// Row maxima of one chunk's (masked) raw scores, reduced over the four 16-lane groups.
+template <int NT>
+__device__ __forceinline__ void pf_rowmax(const f32x4 st[NT][2], float mx[NT]) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    float mx = fmaxf(fmaxf(fmaxf(st[t][0][0], st[t][0][1]), fmaxf(st[t][0][2], st[t][0][3])),
-                     fmaxf(fmaxf(st[t][1][0], st[t][1][1]), fmaxf(st[t][1][2], st[t][1][3])));
-    mx = max_over_groups(mx);
-    const float ms = mx * c;  // -inf stays -inf (c > 0)
-    if (__builtin_amdgcn_ballot_w64(ms > s.m[t] + kRescaleSlack)) {
-      const float m_new = fmaxf(s.m[t], ms);
+    const float m = fmaxf(fmaxf(fmaxf(st[t][0][0], st[t][0][1]), fmaxf(st[t][0][2], st[t][0][3])),
+                          fmaxf(fmaxf(st[t][1][0], st[t][1][1]), fmaxf(st[t][1][2], st[t][1][3])));
+    mx[t] = max_over_groups(m);
+  }
+}
+
+// Online-softmax update from (masked) raw scores and their row maxima; c > 0 so a -inf
+// score gives P = 0. The row test is one compare against thr = (m + kRescaleSlack) / c,
+// kept with nsh = -m and only recomputed when a row's shift moves (a uniform branch). The
+// row sums are taken from the packed (rounded) P with v_dot2 against ones: 4 instructions
+// for 8 scores, and the same P values the P.V contraction uses.
+template <class E, int D, int NT>
+__device__ __forceinline__ void pf_softmax(WaveState<D, NT>& s, const f32x4 st[NT][2], const float mxs[NT], float c,
+                                           u32x4 pt[NT]) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (__builtin_amdgcn_ballot_w64(mxs[t] > s.thr[t])) {
+      const float m_new = fmaxf(s.m[t], mxs[t] * c);  // -inf stays -inf (c > 0)
       // the ballot is wave-wide: a row with no visible key so far keeps m = -inf
-      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(s.m[t] - m_new);
+      const bool empty = m_new == -INFINITY;
+      const float alpha = empty ? 1.f : fast_exp2(s.m[t] - m_new);
       s.l[t] *= alpha;
 #pragma unroll
       for (int i = 0; i < D / 16; ++i) s.acc[t][i] *= alpha;
       s.m[t] = m_new;
+      s.thr[t] = empty ? -INFINITY : (m_new + kRescaleSlack) / c;
+      s.nsh[t] = empty ? 0.f : -m_new;
     }
-    const float nshift = s.m[t] == -INFINITY ? 0.f : -s.m[t];
-    float pv[8], psum = 0.f;
+    float pv[8];
 #pragma unroll
     for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float x = fast_exp2(__builtin_fmaf(st[t][tile][e], c, nshift));
-        pv[4 * tile + e] = x;
-        psum += x;
-      }
-    s.l[t] += psum;
+      for (int e = 0; e < 4; ++e) pv[4 * tile + e] = fast_exp2(__builtin_fmaf(st[t][tile][e], c, s.nsh[t]));
 #pragma unroll
-    for (int w = 0; w < 4; ++w) pt[t][w] = E::pack2(pv[2 * w], pv[2 * w + 1]);
+    for (int w = 0; w < 4; ++w) {
+      pt[t][w] = E::pack2(pv[2 * w], pv[2 * w + 1]);
+      s.l[t] = E::dot2_ones(pt[t][w], s.l[t]);
+    }
   }
 }
 
@@ -773,59 +788,17 @@ struct PrefillLds {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// Block ids and in-page offsets of the two 16-token halves of one 32-key chunk (uniform).
-// An id is -1 for a page past the tile's last key, or an id outside the pool.
-struct ChunkIds {
-  int b[2];
-  int off[2];
-};
-
-// Incremental position of a chunk in the paged layout (no division per step).
-struct ChunkPos {
-  int pg, off;  // page and in-page offset of the chunk's first token
-};
-
-__device__ __forceinline__ void chunk_pos_next(ChunkPos& c, int BS) {
-  c.off += kChunk;
-  while (c.off >= BS) {
-    c.off -= BS;
-    ++c.pg;
-  }
-}
-
-// Scalar loads of the chunk's block ids; the table index is clamped so the load is always
-// in the row (W >= 1), and the id is discarded when the page is past page_end. The table
-// is read through the constant address space (it is never written by a kernel): the loads
-// are scalar and counted by lgkmcnt, so waiting for them never waits for the K/V loads in
-// flight (vmcnt is in order).
-typedef const __attribute__((address_space(4))) int64_t* const_i64_ptr;
-
-__device__ __forceinline__ ChunkIds chunk_ids(const PAParams& p, const int64_t* btrow, const ChunkPos& c,
-                                              int page_end) {
-  ChunkIds r;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int o = c.off + 16 * h;
-    const int pg = o >= p.BS ? c.pg + 1 : c.pg;
-    r.off[h] = o >= p.BS ? o - p.BS : o;
-    const int idx = max(0, min(pg, min(page_end, p.W) - 1));
-    const int64_t blk = ((const_i64_ptr)btrow)[idx];
-    r.b[h] = (pg < page_end && blk >= 0 && blk < p.num_blocks) ? (int)blk : -1;
-  }
-  return r;
-}
-
 // One wave's share of the direct global->LDS loads of a chunk: kLoadsPerWave loads of
 // kRowsPerLoad rows each, all of K or all of V and all in the same 16-token half, so one
-// block id and one uniform base address per wave and chunk; the rows and swizzled slots
-// of the loads are folded into per-lane byte offsets.
+// uniform base address per wave and chunk; the rows and swizzled slots of the loads are
+// folded into per-lane byte offsets (the loads take the SGPR base + VGPR offset form).
 template <int D>
 struct PfLoads {
   using L = PrefillLds<D>;
   static_assert(L::kLoadsPerWave * L::kRowsPerLoad == 16, "a wave's loads cover one 16-token half");
   static_assert(L::kLoadsPerTile % L::kLoadsPerWave == 0, "a wave's loads are all K or all V");
-  const char* cache;  // kc or vc
-  int64_t sb, ss;     // block and slot strides of that cache (elements)
+  const char* cache;  // kc or vc, at this kv head
+  int64_t sb2, ss2;   // block and slot strides of that cache in bytes
   int h;              // the half (0: tokens 0-15 of the chunk, 1: 16-31)
   int dst;            // LDS byte offset of the first load within a stage
   uint32_t loff[L::kLoadsPerWave];
@@ -839,8 +812,8 @@ __device__ __forceinline__ void pf_loads_init(PfLoads<D>& pl, const PAParams& p,
   const int g0 = w * L::kLoadsPerWave;
   const bool v = g0 / L::kLoadsPerTile != 0;
   const int i0 = g0 % L::kLoadsPerTile;
-  pl.sb = v ? p.v_sb : p.k_sb;
-  pl.ss = v ? p.v_ss : p.k_ss;
+  pl.sb2 = 2 * (v ? p.v_sb : p.k_sb);
+  pl.ss2 = 2 * (v ? p.v_ss : p.k_ss);
   pl.cache = (const char*)(v ? p.vc : p.kc) + (int64_t)kvh * (v ? p.v_sh : p.k_sh) * 2;
   pl.h = i0 * L::kRowsPerLoad / 16;
   pl.dst = (v ? L::kTileBytes : 0) + i0 * 1024;
@@ -848,7 +821,7 @@ __device__ __forceinline__ void pf_loads_init(PfLoads<D>& pl, const PAParams& p,
 #pragma unroll
     for (int k = 0; k < L::kLoadsPerWave; ++k) {
       const int row = (i0 + k) * L::kRowsPerLoad + row_in;  // row of the chunk (0..31)
-      pl.loff[k] = (uint32_t)((row % 16) * pl.ss * 2) + 16u * (uint32_t)(slot ^ (row % L::kSlots));
+      pl.loff[k] = (uint32_t)((row % 16) * pl.ss2) + 16u * (uint32_t)(slot ^ (row % L::kSlots));
     }
   } else {
     // V stage layout: blocks b = h (D/16) + i of 512 bytes, block b holding d = 16i .. 16i+15
@@ -859,36 +832,107 @@ __device__ __forceinline__ void pf_loads_init(PfLoads<D>& pl, const PAParams& p,
     for (int k = 0; k < L::kLoadsPerWave; ++k) {
       const int P = 64 * (i0 + k) + lane;
       const int b = P / 32, tok = (P % 32) / 2, chunk = 2 * (b % (D / 16)) + P % 2;
-      pl.loff[k] = (uint32_t)(tok * pl.ss * 2) + 16u * (uint32_t)chunk;
+      pl.loff[k] = (uint32_t)(tok * pl.ss2) + 16u * (uint32_t)chunk;
     }
   }
 }
 
-template <int D>
-__device__ __forceinline__ void pf_issue(char* lds_stage, const PfLoads<D>& pl, const ChunkIds& ids) {
-  using L = PrefillLds<D>;
-  const int b = pl.h ? ids.b[1] : ids.b[0];  // selects, not an indexed load
-  const int off = pl.h ? ids.off[1] : ids.off[0];
-  const int64_t blk = b < 0 ? 0 : b;  // absent page: read block 0, masked later
-  const char* base = pl.cache + (blk * pl.sb + (int64_t)off * pl.ss) * 2;
+// Page descriptors of 64 consecutive chunks (c0 .. c0 + 63 of the tile's key space), one
+// chunk per lane, refreshed every 64 chunks: no address arithmetic per chunk. Lane l holds
+// the byte offset (within this wave's cache, at its kv head) of its half of chunk c0 + l;
+// ok0 / ok1 have bit l set when half 0 / half 1 of that chunk is a page of the pool inside
+// the tile's key range (a missing half is read from block 0 and masked).
+struct PfWindow {
+  uint32_t off_lo, off_hi;  // VGPRs
+  uint64_t ok0, ok1;        // SGPRs
+  int c0;
+  int first_bad;            // first chunk >= c0 with a missing half (c0 + 64 when none)
+};
+
+__device__ __forceinline__ void pf_window(PfWindow& win, const PAParams& p, const int64_t* btrow, int c0, int c_end,
+                                          int page_end, int hmine, int64_t sb2, int64_t ss2) {
+  const int lane = threadIdx.x & 63;
+  const int c = c0 + lane;
+  const int r = p.BS / 16;  // 16-token halves per page (BS % 16 == 0)
+  int id[2];
+  bool ok[2];
+  int off[2];
 #pragma unroll
-  for (int k = 0; k < L::kLoadsPerWave; ++k)
-    __builtin_amdgcn_global_load_lds((const void*)(base + pl.loff[k]), (lds_ptr_t)(lds_stage + pl.dst + k * 1024), 16,
-                                     0, 0);
+  for (int h = 0; h < 2; ++h) {
+    const int hh = 2 * c + h;
+    const int pg = hh / r;
+    off[h] = (hh - pg * r) * 16;
+    int64_t b = -1;
+    if (c < c_end && pg < page_end) b = btrow[pg];
+    ok[h] = b >= 0 && b < p.num_blocks;
+    id[h] = ok[h] ? (int)b : 0;
+  }
+  win.ok0 = __builtin_amdgcn_ballot_w64(ok[0]);
+  win.ok1 = __builtin_amdgcn_ballot_w64(ok[1]);
+  const uint64_t bad = ~(win.ok0 & win.ok1);
+  win.first_bad = c0 + (bad ? (int)__builtin_ctzll(bad) : 64);
+  const int idm = hmine ? id[1] : id[0];
+  const int offm = hmine ? off[1] : off[0];
+  const uint64_t o = (uint64_t)(uint32_t)idm * (uint64_t)sb2 + (uint64_t)(uint32_t)offm * (uint64_t)ss2;
+  win.off_lo = (uint32_t)o;
+  win.off_hi = (uint32_t)(o >> 32);
+  win.c0 = c0;
 }
 
+// DMA of chunk ci (which the window holds) into the stage at LDS byte offset `stage`. The
+// chunk's base address and the lanes' offsets pass through empty asm statements so that
+// instruction selection (per basic block) sees sgpr64 + zext(vgpr32) and picks the
+// SGPR-base + 32-bit VGPR-offset form; otherwise the hoisted 64-bit offsets cost two VGPRs
+// and an add per load.
 template <int D>
-__device__ __forceinline__ void prefill_read_k(KRegs<D>& r, const char* tile) {
+__device__ __forceinline__ void pf_issue(char* lds, int stage, const PfLoads<D>& pl, const PfWindow& win, int ci) {
+  using L = PrefillLds<D>;
+  const int rel = ci - win.c0;
+  const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(win.off_hi, rel) << 32) |
+                     (uint32_t)__builtin_amdgcn_readlane(win.off_lo, rel);
+  uint64_t base = (uint64_t)(uintptr_t)pl.cache + o;
+  asm volatile("" : "+s"(base));
+#pragma unroll
+  for (int k = 0; k < L::kLoadsPerWave; ++k) {
+    uint32_t off = pl.loff[k];
+    asm volatile("" : "+v"(off));  // a 32-bit offset in this block: the load's VGPR operand
+    __builtin_amdgcn_global_load_lds((const void*)((const char*)(uintptr_t)base + off),
+                                     (lds_ptr_t)(lds + stage + pl.dst + k * 1024), 16, 0, 0);
+  }
+}
+
+// Lane byte addresses of the K-operand reads (slot cc of rows n and 16 + n; the XOR swizzle
+// of a row only depends on row % 16, so both 16-row tiles share them).
+template <int D>
+__device__ __forceinline__ void pf_k_lanes(uint32_t ka[D / 32], const char* lds) {
   using L = PrefillLds<D>;
   const int lane = threadIdx.x & 63;
   const int j = lane >> 4, n = lane & 15;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int row = 16 * t + n;
+  for (int cc = 0; cc < D / 32; ++cc)
+    ka[cc] = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds + n * L::kRowBytes +
+             16 * ((4 * cc + j) ^ (n % L::kSlots));
+}
+
+// S^T of one chunk from the K stage, one 16-key tile at a time (16 registers of K operands
+// live instead of 32).
+template <class E, int D, int NT>
+__device__ __forceinline__ void pf_scores_lds(const WaveState<D, NT>& s, const uint32_t ka[D / 32], int stage,
+                                              f32x4 st[NT][2]) {
+  using L = PrefillLds<D>;
+  typedef const __attribute__((address_space(3))) u32x4* lds_u32x4_ptr;
 #pragma unroll
-    for (int cc = 0; cc < D / 32; ++cc) {
-      const int gslot = 4 * cc + j;  // global 16-byte slot: d = 32 cc + 8 j
-      r.k[t][cc] = *(const u32x4*)(tile + row * L::kRowBytes + 16 * (gslot ^ (row % L::kSlots)));
+  for (int tile = 0; tile < 2; ++tile) {
+    u32x4 k[D / 32];
+#pragma unroll
+    for (int cc = 0; cc < D / 32; ++cc)
+      k[cc] = *(lds_u32x4_ptr)(uintptr_t)(ka[cc] + (uint32_t)(stage + 16 * tile * L::kRowBytes));
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int cc = 0; cc < D / 32; ++cc) a = E::mfma(k[cc], s.q[t][cc], a);
+      st[t][tile] = a;
     }
   }
 }
@@ -900,12 +944,70 @@ __device__ __forceinline__ void prefill_read_k(KRegs<D>& r, const char* tile) {
 // output tile i in the same token order as P^T (tokens 4j + e of half 0, then of half 1).
 // The accumulator row 4j + e of tile i is then d = 16i + 4j + e. MASKED zeroes the V of
 // tokens that are absent or at/after data_end (other=0.0 in the reference's masked loads).
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4* lds_i16x4_ptr;
+//
+// The reads are inline asm on purpose. The compiler cannot tell a transpose read of this
+// stage from the LDS DMA still filling the next stages, so for the builtin it inserts
+// s_waitcnt vmcnt(0) first, which drains every K/V load in flight and exposes the full
+// memory latency once per chunk. The kernel orders DMA and reads itself (s_waitcnt vmcnt on
+// its own loads + s_barrier), so the reads are issued as asm and waited for with
+// lgkmcnt(n) counting only the transpose reads issued after the awaited pair: LDS results
+// return in order, so that wait is exact even when other LDS or scalar loads are in flight.
+template <int N>
+struct StaticFor {
+  template <class F>
+  static __device__ __forceinline__ void run(F&& f) {
+    StaticFor<N - 1>::run(f);
+    f(std::integral_constant<int, N - 1>{});
+  }
+};
+template <>
+struct StaticFor<0> {
+  template <class F>
+  static __device__ __forceinline__ void run(F&&) {}
+};
 
-template <class E, int D, int NT, bool MASKED>
-__device__ __forceinline__ void pf_pv(WaveState<D, NT>& s, const char* vtile, const ChunkRef& c, int data_end,
-                                      const u32x4 pt[NT]) {
+template <int D>
+struct VTr {
+  u32x2 lo[D / 16], hi[D / 16];  // tokens 0-15 / 16-31 of the chunk for output tile i
+};
+
+template <int OFF>
+__device__ __forceinline__ void ds_read_tr16_b64(u32x2& dst, uint32_t lds_addr) {
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(dst) : "v"(lds_addr), "i"(OFF));
+}
+
+// Pair i (tile i's two transpose reads) for i in [I0, I1), from the V tile at byte offset
+// VOFF (a compile-time constant, folded into the instructions' offset field) from `base`.
+template <int D, int VOFF, int I0, int I1>
+__device__ __forceinline__ void pf_v_issue(VTr<D>& v, uint32_t base) {
+  StaticFor<I1 - I0>::run([&](auto I) {
+    constexpr int i = I0 + decltype(I)::value;
+    ds_read_tr16_b64<VOFF + 512 * i>(v.lo[i], base);
+    ds_read_tr16_b64<VOFF + 512 * (D / 16 + i)>(v.hi[i], base);
+  });
+}
+
+__device__ __forceinline__ uint32_t lds_lane_addr(const char* tile, int bytes_per_lane) {
+  const int lane = threadIdx.x & 63;
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)tile + (uint32_t)(bytes_per_lane * lane);
+}
+
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tied(u32x2& a, u32x2& b) {
+  // s_waitcnt lgkmcnt(N); the operands tie the awaited registers to the wait so no use of
+  // them is scheduled above it
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+
+// Pairs 0 and 1 were issued by the caller (kVLead pairs ahead); pair i + kVLead is issued
+// right after tile i's MFMAs, so at the wait for pair i exactly the kVLead - 1 later pairs
+// may still be in flight.
+constexpr int kVLead = 2;
+
+template <class E, int D, int NT, bool MASKED, int VOFF>
+__device__ __forceinline__ void pf_pv(WaveState<D, NT>& s, VTr<D>& v, uint32_t vbase, const ChunkRef& c,
+                                      int data_end, const u32x4 pt[NT]) {
+  constexpr int NI = D / 16;
   const int lane = threadIdx.x & 63;
   const int j = lane >> 4;
   uint32_t keep[4] = {~0u, ~0u, ~0u, ~0u};  // dword w: tokens of slots 2w, 2w + 1
@@ -918,20 +1020,19 @@ __device__ __forceinline__ void pf_pv(WaveState<D, NT>& s, const char* vtile, co
       keep[w] = (ok && tok < data_end ? 0x0000ffffu : 0u) | (ok && tok + 1 < data_end ? 0xffff0000u : 0u);
     }
   }
-  const __attribute__((address_space(3))) char* base = (const __attribute__((address_space(3))) char*)vtile + 8 * lane;
-#pragma unroll
-  for (int i = 0; i < D / 16; ++i) {
-    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_ptr)(base + 512 * i));
-    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_ptr)(base + 512 * (D / 16 + i)));
-    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-    u32x4 va = {l2[0], l2[1], h2[0], h2[1]};
+  StaticFor<NI>::run([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    constexpr int later = (i + kVLead <= NI ? kVLead - 1 : NI - 1 - i);  // pairs issued after pair i
+    lgkm_wait_tied<2 * later>(v.lo[i], v.hi[i]);
+    u32x4 va = {v.lo[i][0], v.lo[i][1], v.hi[i][0], v.hi[i][1]};
     if (MASKED) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) va[w] &= keep[w];
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) s.acc[t][i] = E::mfma(va, pt[t], s.acc[t][i]);
-  }
+    if constexpr (i + kVLead < NI) pf_v_issue<D, VOFF, i + kVLead, i + kVLead + 1>(v, vbase);
+  });
 }
 
 // Prefill output / partial rows from the pf_pv accumulator layout (d = 16i + 4j + e).
@@ -974,6 +1075,14 @@ __device__ __forceinline__ void wait_vm() {
 
 // One workgroup's pass over chunks [c_lo, c_hi) of tile t of (seq, kvh): the whole tile
 // (written out) or a piece of it (partial in slot `slot` of the prefill partial arrays).
+//
+// Per chunk a wave waits for its own loads of the chunk, meets the other three at a bare
+// s_barrier (the chunk is complete in LDS and the stage of chunk i - 1 is free), refills that
+// stage with chunk i + 2 and computes chunk i. Three loops keep every accumulator in place
+// (no merge at a branch join): chunks every valid row of the wave sees whole (unmasked, the
+// ring stage of each step known at compile time, so every LDS address is an immediate
+// offset), the chunks on the causal diagonal or with a missing page (masked), then the
+// chunks past the wave's rows (loads and barriers only).
 template <class E, int D>
 __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const SeqView& sv, int R, int seq,
                                              int kvh, int t, int c_lo, int c_hi, int w, bool partial,
@@ -1013,16 +1122,11 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
   const int page_end = (kv_lim + p.BS - 1) / p.BS;
   PfLoads<D> pl;
   pf_loads_init<D>(pl, p, w, kvh);
-  // block ids of steps i .. i + 3: step i + 2 is issued this iteration, step i + 3's ids are
-  // loaded one iteration before they are needed
-  ChunkPos pos;
-  pos.pg = c_lo * kChunk / p.BS;
-  pos.off = c_lo * kChunk % p.BS;
-  ChunkIds id0 = chunk_ids(p, btrow, pos, page_end);
-  chunk_pos_next(pos, p.BS);
-  ChunkIds id1 = chunk_ids(p, btrow, pos, page_end);
-  chunk_pos_next(pos, p.BS);
-  ChunkIds id2 = chunk_ids(p, btrow, pos, page_end);
+  uint32_t ka[D / 32];
+  pf_k_lanes<D>(ka, lds);
+  const uint32_t vbase = lds_lane_addr(lds, 8);
+  PfWindow win;
+  pf_window(win, p, btrow, c_lo, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
 
   // every wave has finished reading the ring (previous tile) before it is refilled
   __builtin_amdgcn_sched_barrier(0);
@@ -1030,14 +1134,19 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
   __builtin_amdgcn_sched_barrier(0);
   const int n = c_hi - c_lo;
   // this wave's rows see chunks c_lo .. c_lo + n_my - 1 only; it keeps taking part in the
-  // loads and barriers of the rest (two loops, so the accumulators never merge at a join)
+  // loads and barriers of the rest
   const int n_my = max(0, min(n, (my_lim + kChunk - 1) / kChunk - c_lo));
-  pf_issue<D>(lds, pl, id0);
-  if (n > 1) pf_issue<D>(lds + L::kStageBytes, pl, id1);
-  // wait for chunk i, then refill the stage chunk i - 1 used with chunk i + 2
-  auto sync_and_issue = [&](int i) {
-    chunk_pos_next(pos, p.BS);
-    const ChunkIds id3 = chunk_ids(p, btrow, pos, page_end);
+  int n_int = max(0, min(n_my, min(lim_all / kChunk, win.first_bad) - c_lo));
+  pf_issue<D>(lds, 0, pl, win, c_lo);
+  if (n > 1) pf_issue<D>(lds, L::kStageBytes, pl, win, c_lo + 1);
+
+  // step i: wait for chunk i, then refill the stage chunk i - 1 used (`next`) with chunk i + 2
+  auto sync = [&](int i, int next) {
+    const int ci2 = c_lo + i + 2;
+    if (i + 2 < n && ci2 - win.c0 >= 64) {  // the window moves on (every 62 chunks)
+      pf_window(win, p, btrow, c_lo + i, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
+      n_int = min(n_int, win.first_bad - c_lo);
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (i + 1 < n)
       wait_vm<L::kLoadsPerWave>();  // chunk i + 1 may stay in flight
@@ -1045,52 +1154,64 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
       wait_vm<0>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    if (i + 2 < n) pf_issue<D>(lds + ((i + 2) % L::kStages) * L::kStageBytes, pl, id2);
+    if (i + 2 < n) pf_issue<D>(lds, next, pl, win, ci2);
     __builtin_amdgcn_sched_barrier(0);
-    const ChunkIds cur = id0;
-    id0 = id1;
-    id1 = id2;
-    id2 = id3;
-    return cur;
   };
-  // chunk i with ids idc: MASKED applies the causal limits and absent pages
-  auto compute = [&](int i, const ChunkIds& idc, auto masked) {
+  // chunk i from the stage at byte offset SOFF + stage (SOFF a compile-time constant)
+  auto compute = [&](int i, int stage, auto soff, auto masked) {
+    constexpr int SOFF = decltype(soff)::value;
     constexpr bool MASKED = decltype(masked)::value;
-    const char* st = lds + (i % L::kStages) * L::kStageBytes;
+    f32x4 sc[NT][2];
+    pf_scores_lds<E, D, NT>(s, ka, SOFF + stage, sc);
     ChunkRef cr;
     cr.tok0 = (c_lo + i) * kChunk;
-    cr.blk[0] = idc.b[0];
-    cr.blk[1] = idc.b[1];
-    KRegs<D> kr;
-    prefill_read_k<D>(kr, st);
-    f32x4 sc[NT][2];
-    pf_scores<E, D, NT>(s, kr, sc);
-    if (MASKED) pf_mask<NT>(sc, s.limit, cr);
-    u32x4 pt[NT];
-    pf_softmax<E, D, NT>(s, sc, c, pt);
-    pf_pv<E, D, NT, MASKED>(s, st + L::kTileBytes, cr, sv.kv_total, pt);
-  };
-  // Three straight-line loops: chunks every valid row sees whole (no masking), the chunks
-  // on the causal diagonal (masked), then the ones this wave's rows cannot see (loads and
-  // barriers only). An absent page among the first moves to the masked loop.
-  const int n_int = max(0, min(n_my, lim_all / kChunk - c_lo));
-  int i = 0;
-  ChunkIds idc;
-  bool synced = false;
-  for (; i < n_int; ++i) {
-    idc = sync_and_issue(i);
-    if (idc.b[0] < 0 || idc.b[1] < 0) {
-      synced = true;
-      break;
+    cr.blk[0] = cr.blk[1] = 0;
+    if (MASKED) {
+      const int rel = c_lo + i - win.c0;
+      cr.blk[0] = (win.ok0 >> rel) & 1 ? 0 : -1;
+      cr.blk[1] = (win.ok1 >> rel) & 1 ? 0 : -1;
+      pf_mask<NT>(sc, s.limit, cr);
     }
-    compute(i, idc, std::false_type{});
+    float mx[NT];
+    pf_rowmax<NT>(sc, mx);
+    // the V transpose reads go out once the scores are in (every QK MFMA has completed, so
+    // the reads may reuse the K registers); their latency hides under the exponentials
+    __builtin_amdgcn_sched_barrier(0);
+    VTr<D> vt;
+    const uint32_t vb = vbase + (uint32_t)stage;
+    pf_v_issue<D, SOFF + L::kTileBytes, 0, kVLead>(vt, vb);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 pt[NT];
+    pf_softmax<E, D, NT>(s, sc, mx, c, pt);
+    pf_pv<E, D, NT, MASKED, SOFF + L::kTileBytes>(s, vt, vb, cr, sv.kv_total, pt);
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, L::kStageBytes>;
+  using S2 = std::integral_constant<int, 2 * L::kStageBytes>;
+  int i = 0;
+  while (i < n_int) {  // unmasked, unrolled by the ring's 3 stages
+    sync(i, 2 * L::kStageBytes);
+    compute(i, 0, S0{}, std::false_type{});
+    if (++i >= n_int) break;
+    sync(i, 0);
+    compute(i, 0, S1{}, std::false_type{});
+    if (++i >= n_int) break;
+    sync(i, L::kStageBytes);
+    compute(i, 0, S2{}, std::false_type{});
+    ++i;
   }
-  for (; i < n_my; ++i) {
-    if (!synced) idc = sync_and_issue(i);
-    synced = false;
-    compute(i, idc, std::true_type{});
+  int stg = i % 3;
+  for (; i < n_my; ++i) {  // masked
+    const int next = stg == 0 ? 2 : stg - 1;
+    sync(i, next * L::kStageBytes);
+    compute(i, stg * L::kStageBytes, S0{}, std::true_type{});
+    stg = stg == 2 ? 0 : stg + 1;
   }
-  for (; i < n; ++i) (void)sync_and_issue(i);
+  for (; i < n; ++i) {  // past this wave's rows: loads and barriers only
+    const int next = stg == 0 ? 2 : stg - 1;
+    sync(i, next * L::kStageBytes);
+    stg = stg == 2 ? 0 : stg + 1;
+  }
   pf_write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, slot * kPrefillRows - wg_row0);
 }
 
