@@ -22,7 +22,10 @@ Also printed in the same JSON line:
   cpu_baseline - the torch restatement of the reference's TorchAttention.forward (fp32, the
                  host's cores) on a bounded sample of the same workload;
   secondary    - the other BASELINE configs (C1, C3 prefill TFLOP/s + decode GB/s, C4 on
-                 unique bytes, C5), timed the same way with fewer steps.
+                 unique bytes, C5), timed the same way with fewer steps;
+  engine_decode_tok_s - Llama-3.2-1B / Llama-3.1-8B decode tokens/s of the engine harness
+                 (kvserve_amd.engine, synthetic weights of the real shapes, HIP-graph decode),
+                 next to the reference's RTX 4090 numbers.
 """
 
 from __future__ import annotations
@@ -210,6 +213,52 @@ def cpu_baseline(idx: int, budget_s: float, seed: int = 0) -> dict:
     }
 
 
+# The reference's published engine decode rates (RTX 4090, graph mode, 512-token prompts):
+# results/rtx4090/decode_graphs.jsonl:1-5 for Llama-3.2-1B; README.md:279 for Llama-3.1-8B.
+REF_DECODE_TOK_S = {"llama_3_2_1b": {1: 253, 8: 1725, 32: 5872, 64: 9588, 128: 14526},
+                    "llama_3_1_8b": {1: 57, 8: 399, 32: 1427}}  # fmt: skip
+
+
+def measure_engine(name: str, batches: list[int], prompt_len: int = 512, steps: int = 50, seed: int = 0) -> dict:
+    """Decode tokens/s of the engine harness with synthetic weights of the model's real shape
+    (bench/bench_decode.py:22-39 of the reference): prefill `batch` prompts of prompt_len
+    tokens, 3 warm-up decode steps, then `steps` timed decode steps replayed from HIP graphs,
+    each step = host metadata + graph replay + logits + greedy argmax read back to the host."""
+    import torch
+
+    from kvserve_amd import HipAttention
+    from kvserve_amd.engine import LLAMA_3_1_8B, LLAMA_3_2_1B
+    from kvserve_amd.engine.model import build_model
+    from kvserve_amd.engine.runner import ModelRunner, Sequence
+
+    cfg = {"llama_3_2_1b": LLAMA_3_2_1B, "llama_3_1_8b": LLAMA_3_1_8B}[name]
+    max_len = prompt_len + steps + 16
+    model = build_model(cfg, "cuda:0", torch.bfloat16, max_len, backend=HipAttention, seed=seed)
+    blocks = max(batches) * -(-max_len // 16) + 16
+    runner = ModelRunner(model, num_blocks=blocks, block_size=16, max_model_len=max_len, use_graphs=True,
+                         max_graph_batch=max(batches))  # fmt: skip
+    out = {}
+    for b in batches:
+        seqs = [Sequence([1000 + (i * 7 + j) % 30000 for j in range(prompt_len)]) for i in range(b)]
+        runner.prefill(seqs)
+        for _ in range(3):
+            runner.decode(seqs)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            runner.decode(seqs)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / steps * 1e3
+        ref = REF_DECODE_TOK_S[name].get(b)
+        out[str(b)] = {"ms_per_step": ms, "tok_s": b / ms * 1e3, "rtx4090_tok_s": ref,
+                       "vs_rtx4090": (b / ms * 1e3) / ref if ref else None}  # fmt: skip
+        for sq in seqs:
+            runner.release(sq)
+    del runner, model
+    torch.cuda.empty_cache()
+    return {"prompt_len": prompt_len, "steps": steps, "weights": "synthetic N(0, 0.02), real shapes", "batches": out}
+
+
 CALIB_ELEMS = 1 << 27  # bf16 elements of the calibration copy: 256 MiB read + 256 MiB written
 
 
@@ -289,6 +338,8 @@ def main() -> int:
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", type=int, default=0, help="run just this config (1-5) and print its record")
     p.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
+    p.add_argument("--no-engine", action="store_true", help="skip the 1B/8B engine decode tokens/s")
+    p.add_argument("--engine-only", action="store_true", help="run just the engine decode tokens/s")
     p.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = p.parse_args()
     if args.pmc_child:
@@ -314,6 +365,11 @@ def main() -> int:
 
     if args.only:
         print(json.dumps(measure(args.only, args.steps, args.warmup, args.prof_iters)), flush=True)
+        return 0
+    engine_batches = {"llama_3_2_1b": [1, 8, 32, 64, 128], "llama_3_1_8b": [1, 8, 32, 64]}
+    if args.engine_only:
+        for name, bs in engine_batches.items():
+            print(json.dumps({name: measure_engine(name, bs)}), flush=True)
         return 0
 
     head = measure(2, args.steps, args.warmup, args.prof_iters)
@@ -376,6 +432,12 @@ def main() -> int:
             print(f"# c{idx}: {r}", file=sys.stderr, flush=True)
             sec[r["workload"]] = {k: v for k, v in r.items() if k not in ("workload", "attn_bytes")}
         record["secondary"] = sec
+    if not args.no_engine:
+        eng = {}
+        for name, bs in engine_batches.items():
+            eng[name] = measure_engine(name, bs)
+            print(f"# engine {name}: {eng[name]}", file=sys.stderr, flush=True)
+        record["engine_decode_tok_s"] = eng
     if not args.no_cpu:
         record["cpu_baseline"] = cpu_baseline(2, args.cpu_budget)
     print(json.dumps(record), flush=True)
