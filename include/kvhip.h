@@ -81,6 +81,34 @@ KVH_API int kvh_reshape_and_cache(const void* k, int64_t k_tok_stride, int64_t k
                           int32_t dtype, void* stream);
 
 /*
+ * rope_and_cache: the step before attention in one pass. From this step's fused QKV
+ * projection qkv [num_tokens, (num_heads + 2 num_kv_heads) head_dim] (token stride
+ * qkv_tok_stride; query heads first, then key heads, then value heads) it computes, for
+ * token t at position p = positions[t] (clamped to the tables),
+ *   x' = x * cos[p] + rotate_half(x) * sin[p],  rotate_half(x) = (-x[D/2:], x[:D/2])
+ * for every query and key head, writes the rotated queries to q_out [num_tokens, num_heads,
+ * head_dim] and scatters the rotated keys and the unrotated values into the paged pool at
+ * slot_mapping[t] like kvh_reshape_and_cache (slots outside the pool are skipped).
+ * cos_table / sin_table: fp32 [max_positions, head_dim] (both halves of a row present).
+ * For 16-bit storage the table values are rounded to the storage type and each product and
+ * the sum are rounded to it, which reproduces PyTorch's separate bf16 / fp16 operations
+ * bit for bit. head_dim must be a multiple of 16 (8 for fp32); pointers 16-byte aligned and
+ * strides multiples of 16 bytes.
+ *
+ * Replaces the split + RoPE of Attention.project (src/kvserve/model.py:84-94, :55-70) and
+ * TorchAttention.write_kv (src/kvserve/attention.py:39-45): one kernel instead of about a
+ * dozen elementwise kernels and two index_put_ scatters per layer.
+ */
+KVH_API int kvh_rope_and_cache(const void* qkv, int64_t qkv_tok_stride, const int64_t* positions,
+                       const float* cos_table, const float* sin_table, int64_t max_positions,
+                       void* q_out, int64_t q_tok_stride, int64_t q_head_stride,
+                       void* k_cache, const int64_t k_cache_strides[3],
+                       void* v_cache, const int64_t v_cache_strides[3],
+                       const int64_t* slot_mapping, int64_t num_tokens, int64_t num_blocks,
+                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                       int32_t dtype, void* stream);
+
+/*
  * Bytes of device workspace kvh_paged_attention needs for this launch shape. Depends only
  * on static quantities (shapes, the block-table width and max_query_len), so a CUDA/HIP
  * graph can allocate it once at capture. May return 0.

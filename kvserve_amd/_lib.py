@@ -35,6 +35,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64p, _vp, _i64p, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp],
     ),
+    "kvh_rope_and_cache": (
+        ctypes.c_int,
+        [
+            _vp, _i64, _vp, _vp, _vp, _i64,  # qkv, positions, cos/sin tables
+            _vp, _i64, _i64,  # q_out
+            _vp, _i64p, _vp, _i64p,  # caches
+            _vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp,  # slots, sizes, dtype, stream
+        ],  # fmt: skip
+    ),
     "kvh_paged_attention_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "kvh_paged_attention": (
         ctypes.c_int,

@@ -110,6 +110,56 @@ class HipAttention:
         )  # fmt: skip
         _lib.check(st, "kvh_reshape_and_cache")
 
+    # Extension beyond the reference's interface: RoPE + QKV split + write_kv in one kernel.
+    fused_rope_cache = True
+
+    @staticmethod
+    def rope_and_cache(
+        qkv: torch.Tensor,
+        positions: torch.Tensor,
+        cos: torch.Tensor,
+        sin: torch.Tensor,
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor,
+        slots: torch.Tensor,
+        num_heads: int,
+        out: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """The step before forward() in one kernel (kvh_rope_and_cache).
+
+        qkv: [T, (num_heads + 2 kv_heads) head_dim], the fused projection (model.py:84-94);
+        positions: int64 [T]; cos, sin: fp32 [max_positions, head_dim] (RotaryEmbedding's
+        tables). Writes RoPE(k) and v into the caches at `slots` (as write_kv) and returns
+        RoPE(q) as [T, num_heads, head_dim] (in `out` if given), bit-identical to the
+        reference's bf16/fp16/fp32 torch operations.
+        """
+        _check_cache(k_cache, v_cache)
+        num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
+        _require(qkv.dim() == 2 and qkv.stride(-1) == 1, "qkv must be [T, (H + 2 Hkv) D] with a contiguous last dim")
+        _require(qkv.shape[1] == (num_heads + 2 * num_kv_heads) * head_dim, "qkv width != (H + 2 Hkv) D")
+        _require(cos.dtype == torch.float32 and sin.dtype == torch.float32, "cos/sin tables must be fp32")
+        _require(cos.dim() == 2 and cos.shape == sin.shape and cos.shape[1] == head_dim, "cos/sin must be [P, D]")
+        _require(cos.is_contiguous() and sin.is_contiguous(), "cos/sin tables must be contiguous")
+        _check_index(positions, "positions", 1)
+        _check_index(slots, "slot_mapping", 1)
+        num_tokens = qkv.shape[0]
+        _require(positions.shape[0] == num_tokens and slots.shape[0] == num_tokens, "one position and slot per token")
+        if out is None:
+            out = torch.empty((num_tokens, num_heads, head_dim), dtype=qkv.dtype, device=qkv.device)
+        _require(out.shape == (num_tokens, num_heads, head_dim) and out.stride(-1) == 1, "out must be [T, H, D]")
+        dtype = _dtype_code(qkv, k_cache, v_cache, out)
+        if num_tokens == 0:
+            return out
+        st = _lib.load().kvh_rope_and_cache(
+            qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+            out.data_ptr(), out.stride(0), out.stride(1),
+            k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(), _lib.i64x3(v_cache.stride()[:3]),
+            slots.data_ptr(), num_tokens, num_blocks, num_heads, num_kv_heads, head_dim, block_size, dtype,
+            _stream_handle(qkv.device),
+        )  # fmt: skip
+        _lib.check(st, "kvh_rope_and_cache")
+        return out
+
     @staticmethod
     def forward(
         q: torch.Tensor,

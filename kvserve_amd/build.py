@@ -22,12 +22,19 @@ LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "libkvhip.so"
 INCLUDE = PKG.parent / "include"
 
-SOURCES = ["kvh_api.hip", "paged_attention.hip", "paged_attention_f32.hip", "reshape_and_cache.hip"]
+SOURCES = [
+    "kvh_api.hip",
+    "paged_attention.hip",
+    "paged_attention_f32.hip",
+    "reshape_and_cache.hip",
+    "rope_and_cache.hip",
+]
 
 # Per-source additions. The MFMA kernels treat scores as finite (masked keys become -inf by
 # selects, never by arithmetic on NaN), so fmaxf needs no sNaN canonicalisation: without
 # -fno-honor-nans every max of an MFMA result costs an extra v_max_f32 x, x, x.
-SOURCE_FLAGS = {"paged_attention.hip": ["-fno-honor-nans"]}
+# rope_and_cache reproduces PyTorch's separately rounded multiply and add: no FMA contraction.
+SOURCE_FLAGS = {"paged_attention.hip": ["-fno-honor-nans"], "rope_and_cache.hip": ["-ffp-contract=off"]}
 
 # -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32 (unreliable on these
 # hosts); the host pass warns that it does not know the feature, which is harmless.

@@ -131,6 +131,37 @@ int kvh_reshape_and_cache(const void* k, int64_t k_tok_stride, int64_t k_head_st
                                   num_kv_heads, head_dim, block_size, eb, vec16, (hipStream_t)stream);
 }
 
+int kvh_rope_and_cache(const void* qkv, int64_t qkv_tok_stride, const int64_t* positions, const float* cos_table,
+                       const float* sin_table, int64_t max_positions, void* q_out, int64_t q_tok_stride,
+                       int64_t q_head_stride, void* k_cache, const int64_t k_cache_strides[3], void* v_cache,
+                       const int64_t v_cache_strides[3], const int64_t* slot_mapping, int64_t num_tokens,
+                       int64_t num_blocks, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                       int32_t block_size, int32_t dtype, void* stream) {
+  if (dtype < KVH_DTYPE_F32 || dtype > KVH_DTYPE_BF16) return KVH_E_DTYPE;
+  if (num_tokens < 0 || num_blocks < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
+      max_positions <= 0)
+    return KVH_E_SHAPE;
+  if (num_tokens > 0x7fffffffLL || num_heads > 65535 || num_kv_heads > 65535) return KVH_E_SHAPE;
+  if (num_tokens == 0) return KVH_OK;
+  if (!qkv || !positions || !cos_table || !sin_table || !q_out || !k_cache || !v_cache || !k_cache_strides ||
+      !v_cache_strides || !slot_mapping)
+    return KVH_E_NULL;
+  const int vec = 16 / elem_bytes(dtype);  // elements per 16-byte vector
+  if (head_dim % (2 * vec) != 0 || head_dim > 1024) return KVH_E_UNSUPPORTED;
+  const int64_t strides[] = {qkv_tok_stride, q_tok_stride, q_head_stride, k_cache_strides[0], k_cache_strides[1],
+                             k_cache_strides[2], v_cache_strides[0], v_cache_strides[1], v_cache_strides[2]};
+  for (int64_t st : strides) {
+    if (st < 0) return KVH_E_SHAPE;
+    if (st % vec) return KVH_E_ALIGN;
+  }
+  if (qkv_tok_stride < (int64_t)(num_heads + 2 * num_kv_heads) * head_dim) return KVH_E_SHAPE;
+  if (!aligned16(qkv) || !aligned16(q_out) || !aligned16(k_cache) || !aligned16(v_cache)) return KVH_E_ALIGN;
+  return launch_rope_and_cache(qkv, qkv_tok_stride, positions, cos_table, sin_table, max_positions, q_out,
+                               q_tok_stride, q_head_stride, k_cache, k_cache_strides, v_cache, v_cache_strides,
+                               slot_mapping, num_tokens, num_blocks, num_heads, num_kv_heads, head_dim, block_size,
+                               dtype, (hipStream_t)stream);
+}
+
 static int check_attention_shape(int64_t num_tokens, int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
                                  int32_t head_dim, int32_t max_blocks_per_seq, int32_t block_size, int32_t dtype) {
   if (dtype < KVH_DTYPE_F32 || dtype > KVH_DTYPE_BF16) return KVH_E_DTYPE;

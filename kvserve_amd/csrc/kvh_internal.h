@@ -84,4 +84,10 @@ int launch_reshape_and_cache(const void* k, int64_t k_ts, int64_t k_hs, const vo
                              const int64_t* slots, int64_t T, int64_t num_blocks, int32_t Hkv, int32_t D,
                              int32_t BS, int32_t elem_bytes, bool vec16, hipStream_t s);
 
+int launch_rope_and_cache(const void* qkv, int64_t qkv_ts, const int64_t* positions, const float* cos_t,
+                          const float* sin_t, int64_t max_pos, void* q_out, int64_t q_ts, int64_t q_hs, void* kc,
+                          const int64_t* kcs, void* vc, const int64_t* vcs, const int64_t* slots, int64_t T,
+                          int64_t num_blocks, int32_t H, int32_t Hkv, int32_t D, int32_t BS, int32_t dtype,
+                          hipStream_t s);
+
 }  // namespace kvh

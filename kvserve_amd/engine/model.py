@@ -103,6 +103,15 @@ class Attention(nn.Module):
         self.backend.write_kv(k_cache, v_cache, k, v, meta.slot_mapping)
         return self.backend.forward(q, k_cache, v_cache, meta, self.scale, out=out)
 
+    def attend_fused(self, qkv, positions, rope: RotaryEmbedding, kv_cache: torch.Tensor, meta: AttentionMetadata,
+                     out: torch.Tensor | None = None):  # fmt: skip
+        """RoPE, QKV split and the cache write in the backend's one kernel, then attention: the
+        same result as project() + attend() (bit for bit) with the RoPE moved out of the piece."""
+        k_cache, v_cache = kv_cache[0], kv_cache[1]
+        q = self.backend.rope_and_cache(qkv, positions, rope.cos, rope.sin, k_cache, v_cache, meta.slot_mapping,
+                                        self.num_heads)  # fmt: skip
+        return self.backend.forward(q, k_cache, v_cache, meta, self.scale, out=out)
+
 
 class MLP(nn.Module):
     def __init__(self, cfg: ModelConfig):
@@ -146,6 +155,8 @@ class LlamaForCausalLM(nn.Module):
         if cfg.tie_word_embeddings:
             self.lm_head.weight = self.embed_tokens.weight
         self.rope = RotaryEmbedding(cfg, max_positions)
+        # a backend with a fused RoPE + cache-write kernel takes the raw QKV projection
+        self.fused_rope = bool(getattr(backend, "fused_rope_cache", False))
 
     @torch.inference_mode()
     def forward(self, input_ids: torch.Tensor, positions: torch.Tensor, kv_caches: torch.Tensor,
@@ -153,7 +164,10 @@ class LlamaForCausalLM(nn.Module):
         """Final hidden states [T, hidden]; kv_caches [layers, 2, blocks, block_size, kv_heads, D]."""
         x, q, k, v = self.piece(0, input_ids, positions, None, None)
         for i, layer in enumerate(self.layers):
-            attn = layer.self_attn.attend(q, k, v, kv_caches[i], meta)
+            if self.fused_rope:
+                attn = layer.self_attn.attend_fused(q, positions, self.rope, kv_caches[i], meta)
+            else:
+                attn = layer.self_attn.attend(q, k, v, kv_caches[i], meta)
             x, q, k, v = self.piece(i + 1, input_ids, positions, x, attn)
         return x
 
@@ -161,7 +175,8 @@ class LlamaForCausalLM(nn.Module):
         """Everything between attention call i - 1 and attention call i (i = 0 .. num_layers):
         finish layer i - 1 (output projection, residual, MLP), start layer i (norm, QKV, RoPE).
         Row-wise, never touches the KV cache (model.py:187-212). Returns (x, q, k, v), or
-        (final hidden states, None, None, None) for the last piece."""
+        (final hidden states, None, None, None) for the last piece. With a fused-RoPE backend
+        the piece stops at the QKV projection: (x, qkv, None, None)."""
         if i == 0:
             x = self.embed_tokens(input_ids)
         else:
@@ -171,7 +186,10 @@ class LlamaForCausalLM(nn.Module):
         if i == len(self.layers):
             return self.norm(x), None, None, None
         layer = self.layers[i]
-        q, k, v = layer.self_attn.project(layer.input_layernorm(x), positions, self.rope)
+        h = layer.input_layernorm(x)
+        if self.fused_rope:
+            return x, layer.self_attn.qkv_proj(h), None, None
+        q, k, v = layer.self_attn.project(h, positions, self.rope)
         return x, q, k, v
 
     @torch.inference_mode()

@@ -7,13 +7,24 @@ TorchAttention (src/kvserve/attention.py:39-82) step by step:
             repeat_interleave(H / Hkv) for GQA, gather padded queries with q_gather,
             mask k_pos <= (seq_len - query_len) + i, scaled_dot_product_attention,
             un-pad with q_valid                                          (:47-82)
-and the padded-layout metadata of build_metadata (src/kvserve/model_runner.py:190-196).
+and the padded-layout metadata of build_metadata (src/kvserve/model_runner.py:190-196),
+plus the RoPE of Attention.project (src/kvserve/model.py:55-70, 84-94) that precedes it.
 """
 
 from __future__ import annotations
 
 import torch
 import torch.nn.functional as F
+
+
+def rope(x: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+    """RotaryEmbedding.forward on one of q / k (src/kvserve/model.py:55-70): the fp32 tables
+    gathered at the positions and cast to x's dtype, then x * cos + rotate_half(x) * sin in
+    x's dtype, rotate_half(x) = cat(-x2, x1)."""
+    cos = cos_table[positions].to(x.dtype)[:, None]
+    sin = sin_table[positions].to(x.dtype)[:, None]
+    x1, x2 = x.chunk(2, dim=-1)
+    return x * cos + torch.cat([-x2, x1], dim=-1) * sin
 
 
 def write_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor):
