@@ -309,29 +309,30 @@ __device__ __forceinline__ void pf_mask(f32x4 st[NT][2], const int limit[NT], co
     }
 }
 
-// Row maxima of one chunk's (masked) raw scores, reduced over the four 16-lane groups.
+// Per-lane maxima of one chunk's (masked) raw scores: the lane's 8 keys of each of its rows.
+// The cross-lane reduction is left to the rare branch that moves a row's shift: a row's
+// maximum passes its threshold exactly when one of its four lanes' maxima does.
 template <int NT>
-__device__ __forceinline__ void pf_rowmax(const f32x4 st[NT][2], float mx[NT]) {
+__device__ __forceinline__ void pf_lanemax(const f32x4 st[NT][2], float mx[NT]) {
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const float m = fmaxf(fmaxf(fmaxf(st[t][0][0], st[t][0][1]), fmaxf(st[t][0][2], st[t][0][3])),
-                          fmaxf(fmaxf(st[t][1][0], st[t][1][1]), fmaxf(st[t][1][2], st[t][1][3])));
-    mx[t] = max_over_groups(m);
-  }
+  for (int t = 0; t < NT; ++t)
+    mx[t] = fmaxf(fmaxf(fmaxf(st[t][0][0], st[t][0][1]), fmaxf(st[t][0][2], st[t][0][3])),
+                  fmaxf(fmaxf(st[t][1][0], st[t][1][1]), fmaxf(st[t][1][2], st[t][1][3])));
 }
 
-// Online-softmax update from (masked) raw scores and their row maxima; c > 0 so a -inf
+// Online-softmax update from (masked) raw scores and per-lane maxima; c > 0 so a -inf
 // score gives P = 0. The row test is one compare against thr = (m + kRescaleSlack) / c,
-// kept with nsh = -m and only recomputed when a row's shift moves (a uniform branch). The
-// row sums are taken from the packed (rounded) P with v_dot2 against ones: 4 instructions
-// for 8 scores, and the same P values the P.V contraction uses.
+// kept with nsh = -m and only recomputed when a row's shift moves (a uniform branch, where
+// the lane maxima are reduced over the row's four lanes). The row sums are taken from the
+// packed (rounded) P with v_dot2 against ones: the same P values the P.V contraction uses.
 template <class E, int D, int NT>
 __device__ __forceinline__ void pf_softmax(WaveState<D, NT>& s, const f32x4 st[NT][2], const float mxs[NT], float c,
                                            u32x4 pt[NT]) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     if (__builtin_amdgcn_ballot_w64(mxs[t] > s.thr[t])) {
-      const float m_new = fmaxf(s.m[t], mxs[t] * c);  // -inf stays -inf (c > 0)
+      const float mrow = max_over_groups(mxs[t]);
+      const float m_new = fmaxf(s.m[t], mrow * c);  // -inf stays -inf (c > 0)
       // the ballot is wave-wide: a row with no visible key so far keeps m = -inf
       const bool empty = m_new == -INFINITY;
       const float alpha = empty ? 1.f : fast_exp2(s.m[t] - m_new);
@@ -1173,7 +1174,7 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
       pf_mask<NT>(sc, s.limit, cr);
     }
     float mx[NT];
-    pf_rowmax<NT>(sc, mx);
+    pf_lanemax<NT>(sc, mx);
     // the V transpose reads go out once the scores are in (every QK MFMA has completed, so
     // the reads may reuse the K registers); their latency hides under the exponentials
     __builtin_amdgcn_sched_barrier(0);
