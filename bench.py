@@ -23,6 +23,8 @@ Also printed in the same JSON line:
                  host's cores) on a bounded sample of the same workload;
   secondary    - the other BASELINE configs (C1, C3 prefill TFLOP/s + decode GB/s, C4 on
                  unique bytes, C5), timed the same way with fewer steps;
+  metadata_prep - per-step input preparation at C2 and C3: the reference's host path vs
+                 block tables resident on the device (kvh_prepare_metadata);
   engine_decode_tok_s - Llama-3.2-1B / Llama-3.1-8B decode tokens/s of the engine harness
                  (kvserve_amd.engine, synthetic weights of the real shapes, HIP-graph decode),
                  next to the reference's RTX 4090 numbers.
@@ -259,6 +261,69 @@ def measure_engine(name: str, batches: list[int], prompt_len: int = 512, steps: 
     return {"prompt_len": prompt_len, "steps": steps, "weights": "synthetic N(0, 0.02), real shapes", "batches": out}
 
 
+def measure_metadata(idx: int, steps: int = 30) -> dict:
+    """Per-step input preparation: the reference's host path (slots per sequence,
+    build_metadata, token and position tensors; model_runner.py:114-125, 165-197) against
+    DeviceMetadata (resident block tables, one packed upload, kvh_prepare_metadata), each
+    step ended by a synchronisation. Every step advances each sequence by its query length
+    (decode: one token; C3's prefill chunks: 384), appending blocks to its table as the
+    reference's allocator would, so the resident tables receive only the new entries."""
+    import torch
+
+    from kvserve_amd import workloads
+    from kvserve_amd.attention import build_metadata
+    from kvserve_amd.metadata import DeviceMetadata
+
+    w = workloads.baseline_config(idx)
+    bs, dev = w.block_size, torch.device("cuda:0")
+    B = len(w.query_lens)
+    seqs = [list(t) for t in w.tables]
+    qlens = list(w.query_lens)
+    growth = [(steps + 2) * q // bs + 2 for q in qlens]
+    spare = iter(())
+    starts = [s - q for s, q in zip(w.seq_lens, w.query_lens)]
+    ids = [(7 * i) % 128000 for i in range(sum(qlens))]
+    width = max(len(t) + g for t, g in zip(seqs, growth))
+    dm = DeviceMetadata(dev, B, width, bs, sum(qlens))
+
+    def advance():
+        for b in range(B):
+            starts[b] += qlens[b]
+            while starts[b] + qlens[b] > len(seqs[b]) * bs:
+                seqs[b].append(next(spare))
+
+    def host_step():
+        slots, pos, seq_lens = [], [], []
+        for t, st, q in zip(seqs, starts, qlens):
+            slots += workloads.slots_for(t, bs, st, q)
+            pos += range(st, st + q)
+            seq_lens.append(st + q)
+        build_metadata(dev, seqs, slots, seq_lens, qlens)
+        torch.tensor(ids, device=dev), torch.tensor(pos, device=dev)
+        torch.cuda.synchronize()
+
+    def device_step():
+        dm.build([(b, seqs[b]) for b in range(B)], starts, qlens, ids)
+        torch.cuda.synchronize()
+
+    out = {"workload": w.name, "batch": B, "tokens": sum(qlens), "max_table": max(len(t) for t in seqs)}
+    saved = (list(starts), [list(t) for t in seqs])
+    for name, fn in (("host_reference_ms", host_step), ("device_ms", device_step)):
+        starts[:], seqs[:] = list(saved[0]), [list(t) for t in saved[1]]
+        spare = iter(range(w.num_blocks, w.num_blocks + sum(growth)))
+        fn()  # first step: the device path uploads every table
+        advance()
+        times = []
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            fn()
+            times.append((time.perf_counter() - t0) * 1e3)
+            advance()
+        out[name] = statistics.median(times)
+    out["speedup"] = out["host_reference_ms"] / out["device_ms"]
+    return out
+
+
 CALIB_ELEMS = 1 << 27  # bf16 elements of the calibration copy: 256 MiB read + 256 MiB written
 
 
@@ -432,6 +497,13 @@ def main() -> int:
             print(f"# c{idx}: {r}", file=sys.stderr, flush=True)
             sec[r["workload"]] = {k: v for k, v in r.items() if k not in ("workload", "attn_bytes")}
         record["secondary"] = sec
+    if not args.no_secondary:
+        meta = {}
+        for idx in (2, 3):
+            m = measure_metadata(idx)
+            print(f"# metadata c{idx}: {m}", file=sys.stderr, flush=True)
+            meta[m.pop("workload")] = m
+        record["metadata_prep"] = meta
     if not args.no_engine:
         eng = {}
         for name, bs in engine_batches.items():

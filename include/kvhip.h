@@ -109,6 +109,38 @@ KVH_API int kvh_rope_and_cache(const void* qkv, int64_t qkv_tok_stride, const in
                        int32_t dtype, void* stream);
 
 /*
+ * prepare_metadata: one step's attention metadata, built on the device from block tables that
+ * stay resident in HBM. table_pool int64 [pool_rows, pool_row_stride] holds one row per live
+ * sequence (its block table, first pool_width entries usable) and persists across calls; the
+ * caller sends only what changed. packed is DEVICE memory (one upload per step), int32:
+ *   [num_seqs][4]     row, start (first position computed this step), q_len, n_blocks
+ *   [num_updates][3]  row, column, block id: set table_pool[row][column] = block id first
+ *                     (at most one update per entry per call)
+ *   [num_tokens]      input token ids, present only when input_ids != NULL
+ * For sequence b (in order; query_start_loc[b] = sum of the earlier q_len) and its token i,
+ * position p = start + i:
+ *   slot_mapping[t] = table_pool[row][p / block_size] * block_size + p % block_size  (-1 when
+ *                     p / block_size >= n_blocks), positions[t] = p, input_ids[t] = token id,
+ *   seq_lens[b] = start + q_len, query_lens[b] = q_len,
+ *   block_tables[b][c] = table_pool[row][c] for c < n_blocks, bt_pad for n_blocks <= c < bt_width.
+ * num_pad_seqs rows follow, each one token: slot pad_slot, position 0, token 0, seq_len 1,
+ * q_len 1, a block-table row of bt_pad. Output arrays hold num_tokens + num_pad_seqs tokens and
+ * num_seqs + num_pad_seqs rows (+1 for query_start_loc); positions, input_ids and query_lens may
+ * be NULL; bt_width = 0 leaves block_tables untouched. Updates outside the pool are skipped.
+ *
+ * Replaces build_metadata (src/kvserve/model_runner.py:165-197, the Triton layout: tables
+ * 0-padded, bt_pad = 0) with the slot formula of KVCacheManager.slots (kv_cache.py:155-169),
+ * and the static-buffer refresh of DecodeGraphRunner.run (src/kvserve/cuda_graph.py:111-134:
+ * scratch padding, bt_pad = scratch block, only the first bt_width columns written).
+ */
+KVH_API int kvh_prepare_metadata(const int32_t* packed, int32_t num_seqs, int32_t num_pad_seqs, int32_t num_updates,
+                         int64_t num_tokens, int64_t* table_pool, int32_t pool_rows, int64_t pool_row_stride,
+                         int32_t pool_width, int64_t* block_tables, int64_t bt_row_stride, int32_t bt_width,
+                         int64_t bt_pad, int64_t* slot_mapping, int64_t* positions, int64_t* input_ids,
+                         int64_t* seq_lens, int64_t* query_lens, int64_t* query_start_loc, int64_t pad_slot,
+                         int32_t block_size, void* stream);
+
+/*
  * Bytes of device workspace kvh_paged_attention needs for this launch shape. Depends only
  * on static quantities (shapes, the block-table width and max_query_len), so a CUDA/HIP
  * graph can allocate it once at capture. May return 0.

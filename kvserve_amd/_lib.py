@@ -44,6 +44,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp,  # slots, sizes, dtype, stream
         ],  # fmt: skip
     ),
+    "kvh_prepare_metadata": (
+        ctypes.c_int,
+        [
+            _vp, _i32, _i32, _i32, _i64,  # packed, num_seqs, num_pad_seqs, num_updates, num_tokens
+            _vp, _i32, _i64, _i32,  # table pool
+            _vp, _i64, _i32, _i64,  # block tables, row stride, width, pad
+            _vp, _vp, _vp, _vp, _vp, _vp,  # slots, positions, input_ids, seq_lens, query_lens, qsl
+            _i64, _i32, _vp,  # pad_slot, block_size, stream
+        ],  # fmt: skip
+    ),
     "kvh_paged_attention_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "kvh_paged_attention": (
         ctypes.c_int,

@@ -24,6 +24,7 @@ INCLUDE = PKG.parent / "include"
 
 SOURCES = [
     "kvh_api.hip",
+    "metadata.hip",
     "paged_attention.hip",
     "paged_attention_f32.hip",
     "reshape_and_cache.hip",

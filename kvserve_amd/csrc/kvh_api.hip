@@ -162,6 +162,51 @@ int kvh_rope_and_cache(const void* qkv, int64_t qkv_tok_stride, const int64_t* p
                                dtype, (hipStream_t)stream);
 }
 
+int kvh_prepare_metadata(const int32_t* packed, int32_t num_seqs, int32_t num_pad_seqs, int32_t num_updates,
+                         int64_t num_tokens, int64_t* table_pool, int32_t pool_rows, int64_t pool_row_stride,
+                         int32_t pool_width, int64_t* block_tables, int64_t bt_row_stride, int32_t bt_width,
+                         int64_t bt_pad, int64_t* slot_mapping, int64_t* positions, int64_t* input_ids,
+                         int64_t* seq_lens, int64_t* query_lens, int64_t* query_start_loc, int64_t pad_slot,
+                         int32_t block_size, void* stream) {
+  if (num_seqs < 0 || num_pad_seqs < 0 || num_updates < 0 || num_tokens < 0 || pool_rows <= 0 || pool_width <= 0 ||
+      pool_row_stride < pool_width || bt_width < 0 || block_size <= 0)
+    return KVH_E_SHAPE;
+  if (num_seqs + (int64_t)num_pad_seqs < 1 || num_seqs + (int64_t)num_pad_seqs > (1 << 24) ||
+      num_tokens > 0x7fffffffLL || num_tokens + num_pad_seqs > 0x7fffffffLL)
+    return KVH_E_SHAPE;
+  if (bt_width > 0 && (!block_tables || bt_row_stride < bt_width)) return block_tables ? KVH_E_SHAPE : KVH_E_NULL;
+  if (!table_pool || !slot_mapping || !seq_lens || !query_start_loc) return KVH_E_NULL;
+  if (!packed && (num_seqs > 0 || num_updates > 0 || (input_ids && num_tokens > 0))) return KVH_E_NULL;
+  const uintptr_t a8 = (uintptr_t)table_pool | (uintptr_t)block_tables | (uintptr_t)slot_mapping |
+                       (uintptr_t)positions | (uintptr_t)input_ids | (uintptr_t)seq_lens | (uintptr_t)query_lens |
+                       (uintptr_t)query_start_loc;
+  if ((a8 & 7u) || ((uintptr_t)packed & 3u)) return KVH_E_ALIGN;
+  MetaParams m{};
+  m.seqs = packed;
+  m.tokens = input_ids ? packed + 4 * (int64_t)num_seqs + 3 * (int64_t)num_updates : nullptr;
+  m.pool = table_pool;
+  m.pool_rows = pool_rows;
+  m.pool_width = pool_width;
+  m.pool_rs = pool_row_stride;
+  m.bt = bt_width > 0 ? block_tables : nullptr;
+  m.bt_rs = bt_row_stride;
+  m.bt_width = bt_width;
+  m.bt_pad = bt_pad;
+  m.slots = slot_mapping;
+  m.positions = positions;
+  m.input_ids = input_ids;
+  m.seq_lens = seq_lens;
+  m.query_lens = query_lens;
+  m.qsl = query_start_loc;
+  m.pad_slot = pad_slot;
+  m.T = num_tokens;
+  m.B = num_seqs;
+  m.P = num_pad_seqs;
+  m.BS = block_size;
+  return launch_prepare_metadata(m, packed ? packed + 4 * (int64_t)num_seqs : nullptr, num_updates,
+                                 (hipStream_t)stream);
+}
+
 static int check_attention_shape(int64_t num_tokens, int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
                                  int32_t head_dim, int32_t max_blocks_per_seq, int32_t block_size, int32_t dtype) {
   if (dtype < KVH_DTYPE_F32 || dtype > KVH_DTYPE_BF16) return KVH_E_DTYPE;

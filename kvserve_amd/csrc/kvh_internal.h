@@ -84,6 +84,30 @@ int launch_reshape_and_cache(const void* k, int64_t k_ts, int64_t k_hs, const vo
                              const int64_t* slots, int64_t T, int64_t num_blocks, int32_t Hkv, int32_t D,
                              int32_t BS, int32_t elem_bytes, bool vec16, hipStream_t s);
 
+// Metadata expansion (kvh_prepare_metadata): pointers into the packed upload and the outputs.
+struct MetaParams {
+  const int32_t* seqs;    // [B][4] row, start, q_len, n_blocks
+  const int32_t* tokens;  // [T] input ids, or null
+  int64_t* pool;          // [pool_rows, pool_rs] resident block tables
+  int32_t pool_rows, pool_width;
+  int64_t pool_rs;
+  int64_t* bt;  // [B + P, bt_rs] batch block tables (first bt_width columns written), or null
+  int64_t bt_rs;
+  int32_t bt_width;
+  int64_t bt_pad;
+  int64_t* slots;      // [T + P]
+  int64_t* positions;  // [T + P] or null
+  int64_t* input_ids;  // [T + P] or null
+  int64_t* seq_lens;   // [B + P]
+  int64_t* query_lens; // [B + P] or null
+  int64_t* qsl;        // [B + P + 1]
+  int64_t pad_slot;
+  int64_t T;  // real tokens
+  int32_t B, P, BS;
+};
+
+int launch_prepare_metadata(const MetaParams& m, const int32_t* updates, int32_t num_updates, hipStream_t s);
+
 int launch_rope_and_cache(const void* qkv, int64_t qkv_ts, const int64_t* positions, const float* cos_t,
                           const float* sin_t, int64_t max_pos, void* q_out, int64_t q_ts, int64_t q_hs, void* kc,
                           const int64_t* kcs, void* vc, const int64_t* vcs, const int64_t* slots, int64_t T,

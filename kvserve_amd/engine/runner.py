@@ -17,6 +17,7 @@ from dataclasses import dataclass, field
 import torch
 
 from kvserve_amd.attention import AttentionMetadata, build_metadata
+from kvserve_amd.metadata import DeviceMetadata, MetaBuffers
 
 
 @dataclass
@@ -62,15 +63,14 @@ class DecodeGraphRunner:
         self.scratch_slot = scratch_block * block_size
         self.sizes = capture_sizes(max_batch)
         self.max_batch = self.sizes[-1]
-        dev = kv_caches.device
         b = self.max_batch
-        self.input_ids = torch.zeros(b, dtype=torch.long, device=dev)
-        self.positions = torch.zeros(b, dtype=torch.long, device=dev)
-        self.slot_mapping = torch.full((b,), self.scratch_slot, dtype=torch.long, device=dev)
-        self.block_tables = torch.full((b, max_blocks_per_seq), scratch_block, dtype=torch.long, device=dev)
-        self.seq_lens = torch.ones(b, dtype=torch.long, device=dev)
-        self.query_lens = torch.ones(b, dtype=torch.long, device=dev)
-        self.query_start_loc = torch.arange(b + 1, dtype=torch.long, device=dev)
+        # static inputs, filled as cuda_graph.py:54-62 fills them
+        self.buf = MetaBuffers(kv_caches.device, b, b, max_blocks_per_seq, slot_fill=self.scratch_slot,
+                               table_fill=scratch_block)  # fmt: skip
+        self.input_ids, self.positions = self.buf.input_ids, self.buf.positions
+        self.slot_mapping, self.block_tables = self.buf.slot_mapping, self.buf.block_tables
+        self.seq_lens, self.query_lens = self.buf.seq_lens, self.buf.query_lens
+        self.query_start_loc = self.buf.query_start_loc
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.outputs: dict[int, torch.Tensor] = {}
 
@@ -129,6 +129,21 @@ class DecodeGraphRunner:
         self.graphs[size].replay()
         return self.outputs[size][:n]
 
+    @torch.inference_mode()
+    def run_device(self, dm: DeviceMetadata, seqs: list[tuple[object, list[int]]], starts: list[int],
+                   input_ids: list[int]) -> torch.Tensor:  # fmt: skip
+        """`run` with the static buffers refreshed on the device from resident block tables
+        (same contents: scratch padding, the first `width` table columns)."""
+        n = len(input_ids)
+        size = self.bucket(n)
+        if size is None:
+            raise ValueError(f"decode batch {n} exceeds the largest captured graph ({self.max_batch})")
+        width = max(len(t) for _, t in seqs)
+        dm.build(seqs, starts, [1] * n, input_ids, buffers=self.buf, pad_seqs=size - n, pad_slot=self.scratch_slot,
+                 table_pad=self.scratch_block, width=width)  # fmt: skip
+        self.graphs[size].replay()
+        return self.outputs[size][:n]
+
 
 class ModelRunner:
     """Owns the model and the paged KV pool; runs prefill and decode steps with greedy
@@ -136,7 +151,8 @@ class ModelRunner:
     graph-capturable)."""
 
     def __init__(self, model, num_blocks: int, block_size: int = 16, max_model_len: int = 4096,
-                 use_graphs: bool = True, max_graph_batch: int = 128, prefill_token_budget: int = 2048):  # fmt: skip
+                 use_graphs: bool = True, max_graph_batch: int = 128, prefill_token_budget: int = 2048,
+                 device_metadata: bool | None = None, max_seqs: int = 1024):  # fmt: skip
         cfg = model.cfg
         p = next(model.parameters())
         self.model = model
@@ -151,6 +167,16 @@ class ModelRunner:
         self.prefill_token_budget = prefill_token_budget
         backend = model.layers[0].self_attn.backend
         self.padded_layout = getattr(backend, "needs_padded_layout", True)
+        # step inputs from block tables kept on the device (kvh_prepare_metadata) unless the
+        # backend needs the torch reference's padded layout, which only the host builds
+        if device_metadata is None:
+            device_metadata = not self.padded_layout and self.device.type == "cuda"
+        if device_metadata and self.padded_layout:
+            raise ValueError("device metadata does not build the padded layout")
+        self.dm = None
+        if device_metadata:
+            self.dm = DeviceMetadata(self.device, max_seqs, -(-max_model_len // block_size), block_size,
+                                     max(prefill_token_budget, max_graph_batch))  # fmt: skip
         self.graphs: DecodeGraphRunner | None = None
         if use_graphs:
             if not getattr(backend, "graph_capturable", False):
@@ -171,6 +197,8 @@ class ModelRunner:
     def release(self, seq: Sequence) -> None:
         self.free_blocks.extend(reversed(seq.block_table))
         seq.block_table = []
+        if self.dm is not None:
+            self.dm.release(id(seq))
 
     def slots(self, seq: Sequence, start: int, n: int) -> list[int]:
         """Slots of positions start .. start + n - 1 (kv_cache.py:155-169)."""
@@ -182,30 +210,43 @@ class ModelRunner:
     def step(self, scheduled: list[tuple[Sequence, int]], force_eager: bool = False) -> dict[int, int]:
         """One forward over `scheduled` (sequence, tokens to compute). Sequences whose context is
         complete after the step get a greedy token, appended to them; returns {index: token}."""
-        ids, pos, slots, seq_lens, query_lens, tables, rows, done = [], [], [], [], [], [], [], []
+        ids, starts, query_lens, tables, rows, done = [], [], [], [], [], []
         for k, (seq, n) in enumerate(scheduled):
             start = seq.num_computed
             if start + n > self.max_model_len:
                 raise ValueError("sequence exceeds max_model_len")
             self._reserve(seq, start + n)
             ids += seq.token_ids[start : start + n]
-            pos += range(start, start + n)
-            slots += self.slots(seq, start, n)
-            seq_lens.append(start + n)
+            starts.append(start)
             query_lens.append(n)
             tables.append(seq.block_table)
             if start + n == seq.num_tokens:
                 rows.append(len(ids) - 1)
                 done.append(k)
         decode = max(query_lens) == 1
-        if self.graphs is not None and decode and not force_eager and len(ids) <= self.graphs.max_batch:
-            hidden = self.graphs.run(ids, pos, slots, tables, seq_lens)
-            self.steps["decode_graph"] += 1
+        use_graph = self.graphs is not None and decode and not force_eager and len(ids) <= self.graphs.max_batch
+        if self.dm is not None:
+            keyed = [(id(seq), seq.block_table) for seq, _ in scheduled]
+            if use_graph:
+                hidden = self.graphs.run_device(self.dm, keyed, starts, ids)
+            else:
+                meta, ids_t, pos_t = self.dm.build(keyed, starts, query_lens, ids)
+                hidden = self.model(ids_t, pos_t, self.kv_caches, meta)
         else:
-            meta = build_metadata(self.device, tables, slots, seq_lens, query_lens, padded_layout=self.padded_layout)
-            hidden = self.model(torch.tensor(ids, device=self.device), torch.tensor(pos, device=self.device),
-                                self.kv_caches, meta)  # fmt: skip
-            self.steps["eager"] += 1
+            # the reference's host path (model_runner.py:114-125, 165-197; cuda_graph.py:111-134)
+            pos, slots, seq_lens = [], [], []
+            for (seq, n), start in zip(scheduled, starts):
+                pos += range(start, start + n)
+                slots += self.slots(seq, start, n)
+                seq_lens.append(start + n)
+            if use_graph:
+                hidden = self.graphs.run(ids, pos, slots, tables, seq_lens)
+            else:
+                meta = build_metadata(self.device, tables, slots, seq_lens, query_lens,
+                                      padded_layout=self.padded_layout)  # fmt: skip
+                hidden = self.model(torch.tensor(ids, device=self.device), torch.tensor(pos, device=self.device),
+                                    self.kv_caches, meta)  # fmt: skip
+        self.steps["decode_graph" if use_graph else "eager"] += 1
         for seq, n in scheduled:
             seq.num_computed += n
         if not rows:

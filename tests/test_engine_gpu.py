@@ -96,3 +96,17 @@ def test_bf16_llama_1b_shape_runs_and_tracks_the_torch_backend(hip_device):
     total = sum(len(x) for x in runs["hip"][1])
     print(f"bf16 greedy token match HIP vs torch backend: {match}/{total}")
     assert runs["hip"][1][0][0] == runs["torch"][1][0][0] or match > 0
+
+
+def test_device_metadata_runner_matches_host_metadata_runner(hip_device):
+    """The same fp32 model run with step inputs from kvh_prepare_metadata (resident block
+    tables) and from the reference's host path: identical tokens, eager and graph steps, with
+    sequences released and their pool rows reused between generations."""
+    out = {}
+    for dev_meta in (True, False):
+        r = ModelRunner(_model(HipAttention, torch.float32), num_blocks=128, max_model_len=1024, use_graphs=True,
+                        max_graph_batch=8, device_metadata=dev_meta, prefill_token_budget=64)  # fmt: skip
+        assert (r.dm is not None) == dev_meta
+        out[dev_meta] = [r.generate(PROMPTS, max_new_tokens=12), r.generate(PROMPTS[::-1], max_new_tokens=12)]
+        assert r.steps["decode_graph"] == 22
+    assert out[True] == out[False]
