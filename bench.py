@@ -84,7 +84,9 @@ def write_bytes(w, elem: int) -> int:
     return 2 * 2 * w.num_tokens * w.num_kv_heads * w.head_dim * elem
 
 
-def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0) -> dict:
+def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0, fp8: bool = False) -> dict:
+    """One BASELINE config, bf16 q/out; fp8: the caches in E4M3 (scales 1 / 0.5, quantized
+    from the same N(0, 1) values), K/V bytes counted at one byte per element."""
     import torch
 
     from kvserve_amd import HipAttention, _lib, last_launch_kernels, workloads
@@ -92,10 +94,22 @@ def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0) -
     w = workloads.baseline_config(idx, seed=seed)
     b = workloads.materialize(w, torch.bfloat16, "cuda:0", seed=seed)
     elem = 2
+    kv_elem = 1 if fp8 else 2
+    kw = {}
+    if fp8:
+        kw = {"k_scale": 1.0, "v_scale": 0.5}
+        for name in ("k_cache", "v_cache"):
+            c, s = getattr(b, name), kw["k_scale" if name == "k_cache" else "v_scale"]
+            c8 = torch.empty(c.shape, dtype=torch.float8_e4m3fn, device=c.device)
+            step_blocks = max(1, (1 << 26) // c[0].numel())
+            for b0 in range(0, c.shape[0], step_blocks):
+                c8[b0 : b0 + step_blocks] = (c[b0 : b0 + step_blocks].float() / s).clamp(-448, 448).to(c8.dtype)
+            setattr(b, name, c8)
+            del c
 
     def step():
-        HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping)
-        return HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale)
+        HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping, **kw)
+        return HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale, **kw)
 
     for _ in range(warmup):
         step()
@@ -112,20 +126,21 @@ def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0) -
     lib = _lib.load()
     ev = HipEvents(5)
     per_kernel: dict[str, list[float]] = {}
-    HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping)
+    HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping, **kw)
     for _ in range(prof_iters):
         lib.kvh_profile_arm(ev.array, 5)
-        HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale)
+        HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale, **kw)
         kinds = last_launch_kernels()
         for k, kind in enumerate(kinds[:4]):
             per_kernel.setdefault(kind, []).append(ev.elapsed_ms(k, k + 1))
     ev.close()
     kernel_ms = {k: statistics.mean(v) for k, v in per_kernel.items()}
 
-    attn_bytes = w.algorithmic_bytes(elem, unique=True)
-    step_bytes = attn_bytes + write_bytes(w, elem)
+    attn_bytes = w.algorithmic_bytes(elem, unique=True, kv_elem_bytes=kv_elem)
+    # the cache write reads 16-bit rows and writes kv_elem-byte rows
+    step_bytes = attn_bytes + write_bytes(w, elem) * (elem + kv_elem) // (2 * elem)
     res = {
-        "workload": w.name,
+        "workload": w.name + ("_fp8kv" if fp8 else ""),
         "ms_per_step": ms_step,
         "step_gbs": step_bytes / (ms_step * 1e-3) / 1e9,
         "attn_bytes": attn_bytes,
@@ -142,13 +157,14 @@ def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0) -
         if "prefill" in kernel_ms:
             res["prefill_tflops"] = pre.flops() / (kernel_ms["prefill"] * 1e-3) / 1e12
             res["prefill_frac_mfma"] = res["prefill_tflops"] / BF16_PEAK_TFLOPS
-        res["decode_kernel_gbs"] = dec.algorithmic_bytes(elem) / (kernel_ms["decode"] * 1e-3) / 1e9
+        res["decode_kernel_gbs"] = dec.algorithmic_bytes(elem, kv_elem_bytes=kv_elem) / (kernel_ms["decode"] * 1e-3) / 1e9
         res["prefill_gflop"] = pre.flops() / 1e9
     else:
         res["decode_kernel_gbs"] = attn_bytes / (kernel_ms["decode"] * 1e-3) / 1e9
         res["attn_gbs"] = attn_bytes / (sum(kernel_ms.values()) * 1e-3) / 1e9
     if idx == 4:
-        res["logical_gbs"] = w.algorithmic_bytes(elem, unique=False) / (sum(kernel_ms.values()) * 1e-3) / 1e9
+        res["logical_gbs"] = (w.algorithmic_bytes(elem, unique=False, kv_elem_bytes=kv_elem)
+                              / (sum(kernel_ms.values()) * 1e-3) / 1e9)  # fmt: skip
     if idx == 5:
         res["tflops"] = w.flops() / (sum(kernel_ms.values()) * 1e-3) / 1e12
     del b
@@ -492,9 +508,10 @@ def main() -> int:
         print(f"# traffic: {t}", file=sys.stderr, flush=True)
     if not args.no_secondary:
         sec = {}
-        for idx in (1, 3, 4, 5):
-            r = measure(idx, max(5, args.steps // 5), 2, max(5, args.prof_iters // 2))
-            print(f"# c{idx}: {r}", file=sys.stderr, flush=True)
+        runs = [(idx, False) for idx in (1, 3, 4, 5)] + [(idx, True) for idx in (2, 3, 4)]
+        for idx, kv8 in runs:
+            r = measure(idx, max(5, args.steps // 5), 2, max(5, args.prof_iters // 2), fp8=kv8)
+            print(f"# c{idx}{' fp8 kv' if kv8 else ''}: {r}", file=sys.stderr, flush=True)
             sec[r["workload"]] = {k: v for k, v in r.items() if k not in ("workload", "attn_bytes")}
         record["secondary"] = sec
     if not args.no_secondary:

@@ -49,7 +49,7 @@ enum kvh_dtype {
 enum kvh_status {
   KVH_OK = 0,
   KVH_E_NULL = -1,        /* a required pointer is NULL */
-  KVH_E_SHAPE = -2,       /* a size is out of range or inconsistent */
+  KVH_E_SHAPE = -2,       /* a size (or an FP8 scale) is out of range or inconsistent */
   KVH_E_DTYPE = -3,       /* unknown dtype */
   KVH_E_ALIGN = -4,       /* pointer/stride not aligned for the vector kernels */
   KVH_E_UNSUPPORTED = -5, /* valid, but not a head_dim/block_size/GQA combination built here */
@@ -81,6 +81,27 @@ KVH_API int kvh_reshape_and_cache(const void* k, int64_t k_tok_stride, int64_t k
                           int32_t dtype, void* stream);
 
 /*
+ * FP8 KV cache. k_cache / v_cache hold OCP FP8 E4M3 bytes (PyTorch's float8_e4m3fn: bias 7,
+ * no infinities, 0x7f / 0xff NaN, largest finite 448), same shape and strides (in elements =
+ * bytes) as a 16-bit cache, with one positive scale per tensor: a value x is stored as
+ *   e4m3(clamp(x / scale, -448, 448))      round to nearest even; NaN stays NaN
+ * which is PyTorch's (x.float() / scale).clamp(-448, 448).to(torch.float8_e4m3fn) bit for bit,
+ * and read back as e4m3 * scale. The reference has no FP8 cache (a roadmap item,
+ * README.md:431); this format halves the bytes decode attention streams.
+ *
+ * reshape_and_cache_fp8: kvh_reshape_and_cache into an E4M3 cache; dtype is that of k and v
+ * (fp32, fp16 or bf16). head_dim % 8 == 0; k, v 16-byte aligned with strides multiples of 16
+ * bytes; caches 8-byte aligned with strides multiples of 8.
+ */
+KVH_API int kvh_reshape_and_cache_fp8(const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                              const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                              void* k_cache, const int64_t k_cache_strides[3],
+                              void* v_cache, const int64_t v_cache_strides[3],
+                              const int64_t* slot_mapping, int64_t num_tokens, int64_t num_blocks,
+                              int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                              int32_t dtype, float k_scale, float v_scale, void* stream);
+
+/*
  * rope_and_cache: the step before attention in one pass. From this step's fused QKV
  * projection qkv [num_tokens, (num_heads + 2 num_kv_heads) head_dim] (token stride
  * qkv_tok_stride; query heads first, then key heads, then value heads) it computes, for
@@ -107,6 +128,17 @@ KVH_API int kvh_rope_and_cache(const void* qkv, int64_t qkv_tok_stride, const in
                        const int64_t* slot_mapping, int64_t num_tokens, int64_t num_blocks,
                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                        int32_t dtype, void* stream);
+
+/* rope_and_cache into E4M3 caches (see reshape_and_cache_fp8): the rotated keys, rounded to
+ * the storage type exactly as above, and the values are stored with k_scale / v_scale. */
+KVH_API int kvh_rope_and_cache_fp8(const void* qkv, int64_t qkv_tok_stride, const int64_t* positions,
+                           const float* cos_table, const float* sin_table, int64_t max_positions,
+                           void* q_out, int64_t q_tok_stride, int64_t q_head_stride,
+                           void* k_cache, const int64_t k_cache_strides[3],
+                           void* v_cache, const int64_t v_cache_strides[3],
+                           const int64_t* slot_mapping, int64_t num_tokens, int64_t num_blocks,
+                           int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                           int32_t dtype, float k_scale, float v_scale, void* stream);
 
 /*
  * prepare_metadata: one step's attention metadata, built on the device from block tables that
@@ -176,6 +208,26 @@ KVH_API int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_h
                         int64_t num_tokens, int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
                         int32_t head_dim, int32_t block_size, int32_t max_query_len, float scale,
                         int32_t dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * kvh_paged_attention over E4M3 caches (see reshape_and_cache_fp8): keys and values are
+ * e4m3 * k_scale and e4m3 * v_scale. q and out are fp16 or bf16 (dtype); the E4M3 values
+ * convert exactly to dtype for the MFMA contractions, k_scale joins the softmax scale and
+ * v_scale the output normalisation, P is rounded to dtype before P.V as in the 16-bit path.
+ * Cache strides must be multiples of 16 bytes; workspace as kvh_paged_attention_workspace_size
+ * for the same shape and dtype.
+ */
+KVH_API int kvh_paged_attention_fp8(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                            const void* k_cache, const int64_t k_cache_strides[3],
+                            const void* v_cache, const int64_t v_cache_strides[3],
+                            int64_t num_blocks,
+                            void* out, int64_t o_tok_stride, int64_t o_head_stride,
+                            const int64_t* block_tables, int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                            const int64_t* seq_lens, const int64_t* query_start_loc,
+                            int64_t num_tokens, int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                            int32_t head_dim, int32_t block_size, int32_t max_query_len, float scale,
+                            float k_scale, float v_scale, int32_t dtype,
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Launch-timing hook for benchmarks (no counterpart in the reference). When armed with an

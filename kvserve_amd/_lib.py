@@ -35,6 +35,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64p, _vp, _i64p, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp],
     ),
+    "kvh_reshape_and_cache_fp8": (
+        ctypes.c_int,
+        [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64p, _vp, _i64p, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _f32,
+         _vp],
+    ),
     "kvh_rope_and_cache": (
         ctypes.c_int,
         [
@@ -42,6 +47,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _i64, _i64,  # q_out
             _vp, _i64p, _vp, _i64p,  # caches
             _vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp,  # slots, sizes, dtype, stream
+        ],  # fmt: skip
+    ),
+    "kvh_rope_and_cache_fp8": (
+        ctypes.c_int,
+        [
+            _vp, _i64, _vp, _vp, _vp, _i64,  # qkv, positions, cos/sin tables
+            _vp, _i64, _i64,  # q_out
+            _vp, _i64p, _vp, _i64p,  # caches
+            _vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _f32, _vp,  # slots, sizes, dtype, scales, stream
         ],  # fmt: skip
     ),
     "kvh_prepare_metadata": (
@@ -64,6 +78,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _i64, _i32,  # block tables
             _vp, _vp,  # seq_lens, query_start_loc
             _i64, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32,  # sizes, scale, dtype
+            _vp, _sz, _vp,  # workspace, stream
+        ],  # fmt: skip
+    ),
+    "kvh_paged_attention_fp8": (
+        ctypes.c_int,
+        [
+            _vp, _i64, _i64,  # q
+            _vp, _i64p, _vp, _i64p, _i64,  # caches, num_blocks
+            _vp, _i64, _i64,  # out
+            _vp, _i64, _i32,  # block tables
+            _vp, _vp,  # seq_lens, query_start_loc
+            _i64, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _f32, _f32, _i32,  # sizes, scales, dtype
             _vp, _sz, _vp,  # workspace, stream
         ],  # fmt: skip
     ),

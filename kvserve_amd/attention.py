@@ -63,6 +63,21 @@ def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
     _require(k_cache.is_cuda and v_cache.is_cuda, "caches must be on a HIP device")
 
 
+# E4M3 KV caches (the *_fp8 entry points): float8_e4m3fn tensors with one scale per tensor.
+FP8 = torch.float8_e4m3fn
+
+
+def _kv_format(k_cache: torch.Tensor, v_cache: torch.Tensor, k_scale: float, v_scale: float) -> bool:
+    """True for E4M3 caches (scales positive and finite); 16-bit / fp32 caches take no scales."""
+    fp8 = k_cache.dtype == FP8
+    _require(v_cache.dtype == k_cache.dtype, f"k/v cache dtypes differ: {k_cache.dtype}, {v_cache.dtype}")
+    if fp8:
+        _require(all(0.0 < float(x) < float("inf") for x in (k_scale, v_scale)), "FP8 scales must be positive, finite")
+    else:
+        _require(k_scale == 1.0 and v_scale == 1.0, "k_scale / v_scale apply to float8_e4m3fn caches only")
+    return fp8
+
+
 def _check_index(t: torch.Tensor, name: str, dim: int) -> None:
     _require(t.dtype == torch.int64, f"{name} must be int64 (got {t.dtype})")
     _require(t.is_cuda, f"{name} must be on the device")
@@ -85,23 +100,41 @@ class HipAttention:
 
     @staticmethod
     def write_kv(
-        k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        slots: torch.Tensor,
+        k_scale: float = 1.0,
+        v_scale: float = 1.0,
     ) -> None:
         """reshape_and_cache: cache.view(-1, Hkv, D)[slots] = k (and v), bit for bit.
 
         caches: [num_blocks, block_size, kv_heads, head_dim]; k, v: [T, kv_heads, head_dim],
         any token/head stride (v is typically a strided view of the fused QKV output).
-        Slots outside the pool are skipped instead of raising.
+        Slots outside the pool are skipped instead of raising. float8_e4m3fn caches store
+        (x / scale).clamp(-448, 448).to(float8_e4m3fn) with the given scales, bit for bit.
         """
         _check_cache(k_cache, v_cache)
+        fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
         num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
         _require(k.dim() == 3 and k.shape == v.shape, "k and v must be [T, kv_heads, head_dim]")
         _require(k.shape[1:] == (num_kv_heads, head_dim), f"k/v rows {tuple(k.shape[1:])} != cache rows")
         _require(k.stride(-1) == 1 and v.stride(-1) == 1, "k/v last dim must be contiguous")
         _check_index(slots, "slot_mapping", 1)
         _require(slots.shape[0] == k.shape[0], "one slot per token")
-        dtype = _dtype_code(k_cache, v_cache, k, v)
         lib = _lib.load()
+        if fp8:
+            dtype = _dtype_code(k, v)
+            st = lib.kvh_reshape_and_cache_fp8(
+                k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+                k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(),
+                _lib.i64x3(v_cache.stride()[:3]), slots.data_ptr(), k.shape[0], num_blocks, num_kv_heads, head_dim,
+                block_size, dtype, float(k_scale), float(v_scale), _stream_handle(k_cache.device),
+            )  # fmt: skip
+            _lib.check(st, "kvh_reshape_and_cache_fp8")
+            return
+        dtype = _dtype_code(k_cache, v_cache, k, v)
         st = lib.kvh_reshape_and_cache(
             k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
             k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(), _lib.i64x3(v_cache.stride()[:3]),
@@ -124,8 +157,11 @@ class HipAttention:
         slots: torch.Tensor,
         num_heads: int,
         out: torch.Tensor | None = None,
+        k_scale: float = 1.0,
+        v_scale: float = 1.0,
     ) -> torch.Tensor:
-        """The step before forward() in one kernel (kvh_rope_and_cache).
+        """The step before forward() in one kernel (kvh_rope_and_cache; float8_e4m3fn caches:
+        kvh_rope_and_cache_fp8, the keys and values stored as write_kv stores them).
 
         qkv: [T, (num_heads + 2 kv_heads) head_dim], the fused projection (model.py:84-94);
         positions: int64 [T]; cos, sin: fp32 [max_positions, head_dim] (RotaryEmbedding's
@@ -134,6 +170,7 @@ class HipAttention:
         reference's bf16/fp16/fp32 torch operations.
         """
         _check_cache(k_cache, v_cache)
+        fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
         num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
         _require(qkv.dim() == 2 and qkv.stride(-1) == 1, "qkv must be [T, (H + 2 Hkv) D] with a contiguous last dim")
         _require(qkv.shape[1] == (num_heads + 2 * num_kv_heads) * head_dim, "qkv width != (H + 2 Hkv) D")
@@ -147,17 +184,22 @@ class HipAttention:
         if out is None:
             out = torch.empty((num_tokens, num_heads, head_dim), dtype=qkv.dtype, device=qkv.device)
         _require(out.shape == (num_tokens, num_heads, head_dim) and out.stride(-1) == 1, "out must be [T, H, D]")
-        dtype = _dtype_code(qkv, k_cache, v_cache, out)
+        dtype = _dtype_code(qkv, out) if fp8 else _dtype_code(qkv, k_cache, v_cache, out)
         if num_tokens == 0:
             return out
-        st = _lib.load().kvh_rope_and_cache(
+        args = [
             qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
             out.data_ptr(), out.stride(0), out.stride(1),
             k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(), _lib.i64x3(v_cache.stride()[:3]),
             slots.data_ptr(), num_tokens, num_blocks, num_heads, num_kv_heads, head_dim, block_size, dtype,
-            _stream_handle(qkv.device),
-        )  # fmt: skip
-        _lib.check(st, "kvh_rope_and_cache")
+        ]  # fmt: skip
+        lib = _lib.load()
+        if fp8:
+            st = lib.kvh_rope_and_cache_fp8(*args, float(k_scale), float(v_scale), _stream_handle(qkv.device))
+            _lib.check(st, "kvh_rope_and_cache_fp8")
+        else:
+            st = lib.kvh_rope_and_cache(*args, _stream_handle(qkv.device))
+            _lib.check(st, "kvh_rope_and_cache")
         return out
 
     @staticmethod
@@ -168,9 +210,13 @@ class HipAttention:
         meta: AttentionMetadata,
         scale: float,
         out: torch.Tensor | None = None,
+        k_scale: float = 1.0,
+        v_scale: float = 1.0,
     ) -> torch.Tensor:
-        """q: [T, H, D]; caches: [num_blocks, block_size, H_kv, D]. Returns [T, H, D] (in `out` if given)."""
+        """q: [T, H, D]; caches: [num_blocks, block_size, H_kv, D]. Returns [T, H, D] (in `out` if given).
+        float8_e4m3fn caches hold keys / values as e4m3 * k_scale / v_scale (q and out bf16 or fp16)."""
         _check_cache(k_cache, v_cache)
+        fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
         num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
         _require(q.dim() == 3 and q.shape[2] == head_dim, "q must be [T, H, head_dim]")
         _require(q.stride(-1) == 1, "q last dim must be contiguous")
@@ -185,7 +231,8 @@ class HipAttention:
         if out is None:
             out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         _require(out.shape == q.shape and out.stride(-1) == 1, "out must match q with a contiguous last dim")
-        dtype = _dtype_code(q, k_cache, v_cache, out)
+        dtype = _dtype_code(q, out) if fp8 else _dtype_code(q, k_cache, v_cache, out)
+        _require(not fp8 or q.dtype != torch.float32, "float8_e4m3fn caches need bf16 or fp16 queries")
         if num_tokens == 0 or num_seqs == 0:
             return out
         lib = _lib.load()
@@ -195,17 +242,22 @@ class HipAttention:
             num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, width, block_size, max_q, dtype
         )
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
-        st = lib.kvh_paged_attention(
+        head = [
             q.data_ptr(), q.stride(0), q.stride(1),
             k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(), _lib.i64x3(v_cache.stride()[:3]),
             num_blocks,
             out.data_ptr(), out.stride(0), out.stride(1),
             tables.data_ptr(), tables.stride(0), width,
             seq_lens.data_ptr(), qsl.data_ptr(),
-            num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_q, float(scale), dtype,
-            ws.data_ptr() if ws is not None else None, ws_bytes, _stream_handle(q.device),
-        )  # fmt: skip
-        _lib.check(st, "kvh_paged_attention")
+            num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_q, float(scale),
+        ]  # fmt: skip
+        tail = [ws.data_ptr() if ws is not None else None, ws_bytes, _stream_handle(q.device)]
+        if fp8:
+            st = lib.kvh_paged_attention_fp8(*head, float(k_scale), float(v_scale), dtype, *tail)
+            _lib.check(st, "kvh_paged_attention_fp8")
+        else:
+            st = lib.kvh_paged_attention(*head, dtype, *tail)
+            _lib.check(st, "kvh_paged_attention")
         return out
 
 

@@ -131,12 +131,49 @@ int kvh_reshape_and_cache(const void* k, int64_t k_tok_stride, int64_t k_head_st
                                   num_kv_heads, head_dim, block_size, eb, vec16, (hipStream_t)stream);
 }
 
-int kvh_rope_and_cache(const void* qkv, int64_t qkv_tok_stride, const int64_t* positions, const float* cos_table,
-                       const float* sin_table, int64_t max_positions, void* q_out, int64_t q_tok_stride,
-                       int64_t q_head_stride, void* k_cache, const int64_t k_cache_strides[3], void* v_cache,
-                       const int64_t v_cache_strides[3], const int64_t* slot_mapping, int64_t num_tokens,
-                       int64_t num_blocks, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-                       int32_t block_size, int32_t dtype, void* stream) {
+int kvh_reshape_and_cache_fp8(const void* k, int64_t k_tok_stride, int64_t k_head_stride, const void* v,
+                              int64_t v_tok_stride, int64_t v_head_stride, void* k_cache,
+                              const int64_t k_cache_strides[3], void* v_cache, const int64_t v_cache_strides[3],
+                              const int64_t* slot_mapping, int64_t num_tokens, int64_t num_blocks,
+                              int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t dtype,
+                              float k_scale, float v_scale, void* stream) {
+  if (dtype < KVH_DTYPE_F32 || dtype > KVH_DTYPE_BF16) return KVH_E_DTYPE;
+  if (num_tokens < 0 || num_blocks < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0)
+    return KVH_E_SHAPE;
+  if (!(k_scale > 0.f && k_scale < INFINITY && v_scale > 0.f && v_scale < INFINITY)) return KVH_E_SHAPE;
+  if (num_tokens > 0x7fffffffLL || (int64_t)num_kv_heads * head_dim / 4 > 0x7fffffffLL) return KVH_E_SHAPE;
+  if (head_dim % 8 != 0) return KVH_E_UNSUPPORTED;
+  if (num_tokens == 0) return KVH_OK;
+  if (!k || !v || !k_cache || !v_cache || !k_cache_strides || !v_cache_strides || !slot_mapping) return KVH_E_NULL;
+  const int vec = 16 / elem_bytes(dtype);  // source elements per 16 bytes
+  const int64_t src[] = {k_tok_stride, k_head_stride, v_tok_stride, v_head_stride};
+  const int64_t dst[] = {k_cache_strides[0], k_cache_strides[1], k_cache_strides[2],
+                         v_cache_strides[0], v_cache_strides[1], v_cache_strides[2]};
+  for (int64_t st : src) {
+    if (st < 0) return KVH_E_SHAPE;
+    if (st % vec) return KVH_E_ALIGN;
+  }
+  for (int64_t st : dst) {
+    if (st < 0) return KVH_E_SHAPE;
+    if (st % 8) return KVH_E_ALIGN;  // 8-byte stores of E4M3 bytes
+  }
+  if (!aligned16(k) || !aligned16(v) || ((uintptr_t)k_cache & 7u) || ((uintptr_t)v_cache & 7u)) return KVH_E_ALIGN;
+  return launch_reshape_and_cache_fp8(k, k_tok_stride, k_head_stride, v, v_tok_stride, v_head_stride, k_cache,
+                                      k_cache_strides, v_cache, v_cache_strides, slot_mapping, num_tokens, num_blocks,
+                                      num_kv_heads, head_dim, block_size, dtype, k_scale, v_scale,
+                                      (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+static int rope_and_cache_impl(const void* qkv, int64_t qkv_tok_stride, const int64_t* positions,
+                               const float* cos_table, const float* sin_table, int64_t max_positions, void* q_out,
+                               int64_t q_tok_stride, int64_t q_head_stride, void* k_cache,
+                               const int64_t k_cache_strides[3], void* v_cache, const int64_t v_cache_strides[3],
+                               const int64_t* slot_mapping, int64_t num_tokens, int64_t num_blocks, int32_t num_heads,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t dtype, bool kv8,
+                               float k_scale, float v_scale, void* stream) {
+  if (kv8 && !(k_scale > 0.f && k_scale < INFINITY && v_scale > 0.f && v_scale < INFINITY)) return KVH_E_SHAPE;
   if (dtype < KVH_DTYPE_F32 || dtype > KVH_DTYPE_BF16) return KVH_E_DTYPE;
   if (num_tokens < 0 || num_blocks < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
       max_positions <= 0)
@@ -146,7 +183,7 @@ int kvh_rope_and_cache(const void* qkv, int64_t qkv_tok_stride, const int64_t* p
   if (!qkv || !positions || !cos_table || !sin_table || !q_out || !k_cache || !v_cache || !k_cache_strides ||
       !v_cache_strides || !slot_mapping)
     return KVH_E_NULL;
-  const int vec = 16 / elem_bytes(dtype);  // elements per 16-byte vector
+  const int vec = 16 / elem_bytes(dtype);  // elements per 16-byte vector (E4M3 cache: vec bytes)
   if (head_dim % (2 * vec) != 0 || head_dim > 1024) return KVH_E_UNSUPPORTED;
   const int64_t strides[] = {qkv_tok_stride, q_tok_stride, q_head_stride, k_cache_strides[0], k_cache_strides[1],
                              k_cache_strides[2], v_cache_strides[0], v_cache_strides[1], v_cache_strides[2]};
@@ -155,11 +192,40 @@ int kvh_rope_and_cache(const void* qkv, int64_t qkv_tok_stride, const int64_t* p
     if (st % vec) return KVH_E_ALIGN;
   }
   if (qkv_tok_stride < (int64_t)(num_heads + 2 * num_kv_heads) * head_dim) return KVH_E_SHAPE;
-  if (!aligned16(qkv) || !aligned16(q_out) || !aligned16(k_cache) || !aligned16(v_cache)) return KVH_E_ALIGN;
+  const bool caches_ok = kv8 ? !(((uintptr_t)k_cache | (uintptr_t)v_cache) & (uintptr_t)(vec - 1))
+                             : aligned16(k_cache) && aligned16(v_cache);
+  if (!aligned16(qkv) || !aligned16(q_out) || !caches_ok) return KVH_E_ALIGN;
   return launch_rope_and_cache(qkv, qkv_tok_stride, positions, cos_table, sin_table, max_positions, q_out,
                                q_tok_stride, q_head_stride, k_cache, k_cache_strides, v_cache, v_cache_strides,
                                slot_mapping, num_tokens, num_blocks, num_heads, num_kv_heads, head_dim, block_size,
-                               dtype, (hipStream_t)stream);
+                               dtype, kv8, k_scale, v_scale, (hipStream_t)stream);
+}
+
+extern "C" {
+
+int kvh_rope_and_cache(const void* qkv, int64_t qkv_tok_stride, const int64_t* positions, const float* cos_table,
+                       const float* sin_table, int64_t max_positions, void* q_out, int64_t q_tok_stride,
+                       int64_t q_head_stride, void* k_cache, const int64_t k_cache_strides[3], void* v_cache,
+                       const int64_t v_cache_strides[3], const int64_t* slot_mapping, int64_t num_tokens,
+                       int64_t num_blocks, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                       int32_t block_size, int32_t dtype, void* stream) {
+  return rope_and_cache_impl(qkv, qkv_tok_stride, positions, cos_table, sin_table, max_positions, q_out,
+                             q_tok_stride, q_head_stride, k_cache, k_cache_strides, v_cache, v_cache_strides,
+                             slot_mapping, num_tokens, num_blocks, num_heads, num_kv_heads, head_dim, block_size,
+                             dtype, false, 1.f, 1.f, stream);
+}
+
+int kvh_rope_and_cache_fp8(const void* qkv, int64_t qkv_tok_stride, const int64_t* positions,
+                           const float* cos_table, const float* sin_table, int64_t max_positions, void* q_out,
+                           int64_t q_tok_stride, int64_t q_head_stride, void* k_cache,
+                           const int64_t k_cache_strides[3], void* v_cache, const int64_t v_cache_strides[3],
+                           const int64_t* slot_mapping, int64_t num_tokens, int64_t num_blocks, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t dtype, float k_scale,
+                           float v_scale, void* stream) {
+  return rope_and_cache_impl(qkv, qkv_tok_stride, positions, cos_table, sin_table, max_positions, q_out,
+                             q_tok_stride, q_head_stride, k_cache, k_cache_strides, v_cache, v_cache_strides,
+                             slot_mapping, num_tokens, num_blocks, num_heads, num_kv_heads, head_dim, block_size,
+                             dtype, true, k_scale, v_scale, stream);
 }
 
 int kvh_prepare_metadata(const int32_t* packed, int32_t num_seqs, int32_t num_pad_seqs, int32_t num_updates,
@@ -240,14 +306,18 @@ size_t kvh_paged_attention_workspace_size(int64_t num_tokens, int32_t num_seqs, 
       .ws_bytes;
 }
 
-int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride, const void* k_cache,
-                        const int64_t k_cache_strides[3], const void* v_cache, const int64_t v_cache_strides[3],
-                        int64_t num_blocks, void* out, int64_t o_tok_stride, int64_t o_head_stride,
-                        const int64_t* block_tables, int64_t bt_row_stride, int32_t max_blocks_per_seq,
-                        const int64_t* seq_lens, const int64_t* query_start_loc, int64_t num_tokens, int32_t num_seqs,
-                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                        int32_t max_query_len, float scale, int32_t dtype, void* workspace, size_t workspace_bytes,
-                        void* stream) {
+}  // extern "C"
+
+// kvh_paged_attention and kvh_paged_attention_fp8 (kv8: E4M3 caches with scales k_scale, v_scale).
+static int paged_attention_impl(const void* q, int64_t q_tok_stride, int64_t q_head_stride, const void* k_cache,
+                                const int64_t k_cache_strides[3], const void* v_cache,
+                                const int64_t v_cache_strides[3], int64_t num_blocks, void* out, int64_t o_tok_stride,
+                                int64_t o_head_stride, const int64_t* block_tables, int64_t bt_row_stride,
+                                int32_t max_blocks_per_seq, const int64_t* seq_lens, const int64_t* query_start_loc,
+                                int64_t num_tokens, int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t block_size, int32_t max_query_len, float scale,
+                                int32_t dtype, bool kv8, float k_scale, float v_scale, void* workspace,
+                                size_t workspace_bytes, void* stream) {
   // the timing hook covers exactly one call, whatever its outcome
   LaunchLog log;
   void* armed[8];
@@ -265,13 +335,18 @@ int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stri
     return KVH_E_NULL;
   // num_blocks >= 1: the kernels read block 0 in place of an absent tile (and mask it out)
   if (num_blocks < 1 || bt_row_stride < max_blocks_per_seq) return KVH_E_SHAPE;
+  if (kv8) {
+    if (dtype == KVH_DTYPE_F32) return KVH_E_UNSUPPORTED;  // E4M3 caches feed the 16-bit MFMA path
+    if (!(k_scale > 0.f && k_scale < INFINITY && v_scale > 0.f && v_scale < INFINITY)) return KVH_E_SHAPE;
+  }
   const int64_t strides[] = {q_tok_stride, q_head_stride, o_tok_stride, o_head_stride,
                              k_cache_strides[0], k_cache_strides[1], k_cache_strides[2],
                              v_cache_strides[0], v_cache_strides[1], v_cache_strides[2]};
   const int vec_elems = dtype == KVH_DTYPE_F32 ? 4 : 8;
-  for (int64_t s : strides) {
-    if (s < 0) return KVH_E_SHAPE;
-    if (s % vec_elems) return KVH_E_ALIGN;
+  for (int i = 0; i < 10; ++i) {
+    if (strides[i] < 0) return KVH_E_SHAPE;
+    // E4M3 cache rows are read 16 bytes at a time: 16 one-byte elements
+    if (strides[i] % (kv8 && i >= 4 ? 16 : vec_elems)) return KVH_E_ALIGN;
   }
   if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out)) return KVH_E_ALIGN;
 
@@ -308,7 +383,8 @@ int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stri
   p.G = plan.G;
   p.BS = block_size;
   p.scale = scale;
-  p.qk_scale = scale * kLog2e;
+  p.qk_scale = scale * kLog2e * (kv8 ? k_scale : 1.f);
+  p.v_scale = kv8 ? v_scale : 1.f;
   p.QS = plan.QS;
   p.RS = plan.RS;
   p.HGW = plan.HGW;
@@ -346,10 +422,42 @@ int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stri
   if (dtype == KVH_DTYPE_F32)
     st = launch_paged_attention_f32(p, head_dim, max_query_len < 1 ? 1 : max_query_len, s, log);
   else
-    st = launch_paged_attention_mfma(p, plan, head_dim, dtype, s, log);
+    st = launch_paged_attention_mfma(p, plan, head_dim, dtype, kv8, max_query_len < 1 ? 1 : max_query_len, s, log);
   g_prof.last_count = log.launched;
   for (int i = 0; i < 8; ++i) g_prof.last_kinds[i] = log.kinds[i];
   return st;
+}
+
+extern "C" {
+
+int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride, const void* k_cache,
+                        const int64_t k_cache_strides[3], const void* v_cache, const int64_t v_cache_strides[3],
+                        int64_t num_blocks, void* out, int64_t o_tok_stride, int64_t o_head_stride,
+                        const int64_t* block_tables, int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                        const int64_t* seq_lens, const int64_t* query_start_loc, int64_t num_tokens, int32_t num_seqs,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        int32_t max_query_len, float scale, int32_t dtype, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  return paged_attention_impl(q, q_tok_stride, q_head_stride, k_cache, k_cache_strides, v_cache, v_cache_strides,
+                              num_blocks, out, o_tok_stride, o_head_stride, block_tables, bt_row_stride,
+                              max_blocks_per_seq, seq_lens, query_start_loc, num_tokens, num_seqs, num_heads,
+                              num_kv_heads, head_dim, block_size, max_query_len, scale, dtype, false, 1.f, 1.f,
+                              workspace, workspace_bytes, stream);
+}
+
+int kvh_paged_attention_fp8(const void* q, int64_t q_tok_stride, int64_t q_head_stride, const void* k_cache,
+                            const int64_t k_cache_strides[3], const void* v_cache, const int64_t v_cache_strides[3],
+                            int64_t num_blocks, void* out, int64_t o_tok_stride, int64_t o_head_stride,
+                            const int64_t* block_tables, int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                            const int64_t* seq_lens, const int64_t* query_start_loc, int64_t num_tokens,
+                            int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                            int32_t block_size, int32_t max_query_len, float scale, float k_scale, float v_scale,
+                            int32_t dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  return paged_attention_impl(q, q_tok_stride, q_head_stride, k_cache, k_cache_strides, v_cache, v_cache_strides,
+                              num_blocks, out, o_tok_stride, o_head_stride, block_tables, bt_row_stride,
+                              max_blocks_per_seq, seq_lens, query_start_loc, num_tokens, num_seqs, num_heads,
+                              num_kv_heads, head_dim, block_size, max_query_len, scale, dtype, true, k_scale, v_scale,
+                              workspace, workspace_bytes, stream);
 }
 
 int kvh_profile_arm(void* const* events, int32_t num_events) {

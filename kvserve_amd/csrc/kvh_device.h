@@ -36,6 +36,12 @@ struct BF16 {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
   }
   static __device__ __forceinline__ float to_f32(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
+  // Two E4M3 values (bytes 0-1 of w, or 2-3 when HI) as a packed bf16 pair, low byte in the
+  // low half; every E4M3 value is exact in bf16, so the conversion (scale 1) rounds nothing.
+  template <bool HI>
+  static __device__ __forceinline__ uint32_t from_fp8x2(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, HI));
+  }
   // acc + lo + hi of a packed pair (v_dot2_f32_bf16 against {1, 1})
   static __device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -58,12 +64,36 @@ struct F16 {
   static __device__ __forceinline__ float to_f32(uint16_t x) {
     return (float)__builtin_bit_cast(_Float16, x);
   }
+  // Two E4M3 values as a packed fp16 pair (exact, as for bf16).
+  template <bool HI>
+  static __device__ __forceinline__ uint32_t from_fp8x2(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, HI));
+  }
   // acc + lo + hi of a packed pair (v_dot2_f32_f16 against {1, 1})
   static __device__ __forceinline__ float dot2_ones(uint32_t x, float acc) {
     typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), __builtin_bit_cast(f16x2_t, 0x3c003c00u), acc, false);
   }
 };
+
+// OCP FP8 E4M3 (float8_e4m3fn, bias 7, no infinities, 0x7f / 0xff NaN, largest finite 448):
+// the KV-cache storage format of the *_fp8 entry points. A value x is stored as
+// e4m3(clamp(x / scale, -448, 448)) with round-to-nearest-even, PyTorch's
+// (x.float() / scale).clamp(-448, 448).to(torch.float8_e4m3fn): an IEEE fp32 division, then
+// a clamp that lets NaN through, then the conversion.
+constexpr float kFp8Max = 448.f;
+
+__device__ __forceinline__ float fp8_prep(float x, float scale) {
+  const float y = x / scale;
+  return y > kFp8Max ? kFp8Max : (y < -kFp8Max ? -kFp8Max : y);
+}
+
+// Four prepared values to four E4M3 bytes (a in byte 0); v_cvt_pk_fp8_f32 rounds to nearest
+// even, and the inputs are already within range.
+__device__ __forceinline__ uint32_t fp8_pack4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
 
 // Interleave the low (SEL = 0) or high (SEL = 1) 16-bit halves of two dwords:
 // result = {half(a), half(b)} with half(a) in the low 16 bits.

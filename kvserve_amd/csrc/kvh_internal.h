@@ -37,12 +37,14 @@ struct PAParams {
   int64_t T;
   int32_t W, B, H, Hkv, G, BS;
   float scale;     // softmax scale as given
-  float qk_scale;  // scale * log2(e): scores are kept in the exp2 domain
+  float qk_scale;  // scale * log2(e) (* the K scale of an E4M3 cache): scores in the exp2 domain
   int32_t QS;      // sequences with 0 < q_len <= QS are decode class (stream-K kernel)
   int32_t RS;      // query rows of a decode-class sequence at most: QS * G
   int32_t HGW;     // kv heads (waves) per work unit of the decode kernel: 8, 4, 2 or 1
   int32_t NU;      // work units the decode launch provides (waves / HGW)
-  int32_t NUP;     // work units (workgroups) of the prefill launch, 0 when none
+  int32_t NUP;     // work units (workgroups) of the prefill launch (16-bit cache), else 0
+  int32_t PLAN;    // 1: workgroup 0 of the decode launch writes the prefill plan
+  float v_scale;   // factor of every output row: the V scale of an E4M3 cache, else 1
   float* ws_acc;   // [slots, HGW, RS, D] unnormalised partial outputs of split decode segments
   float* ws_ml;    // [slots, HGW, RS, 2] running max (exp2 domain) and sum of each partial
   float* ws_pacc;  // [2 kMaxPrefillUnits, kPrefillRows, D] partial outputs of split prefill tiles
@@ -76,8 +78,8 @@ struct LaunchLog {
   void after_launch(int kind, hipStream_t s);
 };
 
-int launch_paged_attention_mfma(PAParams& p, const Plan& plan, int32_t D, int32_t dtype, hipStream_t s,
-                                LaunchLog& log);
+int launch_paged_attention_mfma(PAParams& p, const Plan& plan, int32_t D, int32_t dtype, bool kv8, int32_t max_q,
+                                hipStream_t s, LaunchLog& log);
 int launch_paged_attention_f32(const PAParams& p, int32_t D, int32_t max_q, hipStream_t s, LaunchLog& log);
 int launch_reshape_and_cache(const void* k, int64_t k_ts, int64_t k_hs, const void* v, int64_t v_ts,
                              int64_t v_hs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs,
@@ -112,6 +114,10 @@ int launch_rope_and_cache(const void* qkv, int64_t qkv_ts, const int64_t* positi
                           const float* sin_t, int64_t max_pos, void* q_out, int64_t q_ts, int64_t q_hs, void* kc,
                           const int64_t* kcs, void* vc, const int64_t* vcs, const int64_t* slots, int64_t T,
                           int64_t num_blocks, int32_t H, int32_t Hkv, int32_t D, int32_t BS, int32_t dtype,
-                          hipStream_t s);
+                          bool kv8, float k_scale, float v_scale, hipStream_t s);
+int launch_reshape_and_cache_fp8(const void* k, int64_t k_ts, int64_t k_hs, const void* v, int64_t v_ts,
+                                 int64_t v_hs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs,
+                                 const int64_t* slots, int64_t T, int64_t num_blocks, int32_t Hkv, int32_t D,
+                                 int32_t BS, int32_t dtype, float k_scale, float v_scale, hipStream_t s);
 
 }  // namespace kvh

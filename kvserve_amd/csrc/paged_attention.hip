@@ -95,6 +95,20 @@ struct VRegs {
   uint32_t v[8][VW / 2];             // token t8 = 4 tile + e  <->  chunk token 16 tile + 4j + e
 };
 
+// The same chunk from an E4M3 cache (KV8), as loaded; converted to 16-bit MFMA operands at
+// use. K: 16 bytes per lane per pair of operands: lane (j, n) holds token 16t + n, bytes
+// d = 64c + 16j .. +15, and operand 2c + h takes d = 64c + 16j + 8h .. +7 (the query operand
+// uses the same k-slot order). V: lane (j, m) holds d = VW m .. VW m + VW - 1 of 8 tokens.
+template <int D>
+struct KRegs8 {
+  u32x4 k[2][D / 64];
+};
+template <int D>
+struct VRegs8 {
+  static constexpr int VW = D / 16;
+  uint32_t v[8][VW / 4];  // token t8 as in VRegs, 4 E4M3 values per dword
+};
+
 // Uniform description of a chunk: first token and the block of each 16-token tile.
 struct ChunkRef {
   int tok0;
@@ -119,13 +133,18 @@ struct LaneOffsets {
   uint32_t v;  // (4j * v_ss + VW n) * 2
 };
 
-template <int D>
+template <int D, bool KV8 = false>
 __device__ __forceinline__ LaneOffsets lane_offsets(const PAParams& p) {
   const int lane = threadIdx.x & 63;
   const int j = lane >> 4, n = lane & 15;
   LaneOffsets o;
-  o.k = (uint32_t)(n * (uint32_t)p.k_ss + 8 * j) * 2u;
-  o.v = (uint32_t)(4 * j * (uint32_t)p.v_ss + (D / 16) * n) * 2u;
+  if (KV8) {  // one byte per element
+    o.k = (uint32_t)(n * (uint32_t)p.k_ss + 16 * j);
+    o.v = (uint32_t)(4 * j * (uint32_t)p.v_ss + (D / 16) * n);
+  } else {
+    o.k = (uint32_t)(n * (uint32_t)p.k_ss + 8 * j) * 2u;
+    o.v = (uint32_t)(4 * j * (uint32_t)p.v_ss + (D / 16) * n) * 2u;
+  }
   return o;
 }
 
@@ -170,6 +189,48 @@ __device__ __forceinline__ void load_v(VRegs<D>& r, const PAParams& p, const Chu
   }
 }
 
+template <int D>
+__device__ __forceinline__ void load_k(KRegs8<D>& r, const PAParams& p, const ChunkRef& c, int kvh, uint32_t k_lane) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t blk = c.blk[t] >= 0 ? c.blk[t] : 0;
+    const int slot0 = (c.tok0 + 16 * t) % p.BS;
+    const char* page = (const char*)p.kc + blk * p.k_sb + (int64_t)kvh * p.k_sh + (int64_t)slot0 * p.k_ss;
+#pragma unroll
+    for (int cc = 0; cc < D / 64; ++cc) r.k[t][cc] = *(const u32x4*)(page + k_lane + 64 * cc);
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void load_v(VRegs8<D>& r, const PAParams& p, const ChunkRef& c, int kvh, uint32_t v_lane) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t blk = c.blk[t] >= 0 ? c.blk[t] : 0;
+    const int slot0 = (c.tok0 + 16 * t) % p.BS;
+    const char* page = (const char*)p.vc + blk * p.v_sb + (int64_t)kvh * p.v_sh + (int64_t)slot0 * p.v_ss;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const char* src = page + (int64_t)e * p.v_ss + v_lane;
+      if constexpr (D == 128) {
+        const u32x2 x = *(const u32x2*)src;
+        r.v[4 * t + e][0] = x[0];
+        r.v[4 * t + e][1] = x[1];
+      } else {
+        r.v[4 * t + e][0] = *(const uint32_t*)src;
+      }
+    }
+  }
+}
+
+// K operand cc of tile `tile` of an E4M3 chunk, converted (exactly) to E's type.
+template <class E, int D>
+__device__ __forceinline__ u32x4 k_operand(const KRegs8<D>& r, int tile, int cc) {
+  const u32x4 w = r.k[tile][cc >> 1];
+  const uint32_t a = w[2 * (cc & 1)], b = w[2 * (cc & 1) + 1];
+  return u32x4{E::template from_fp8x2<false>(a), E::template from_fp8x2<true>(a), E::template from_fp8x2<false>(b),
+               E::template from_fp8x2<true>(b)};
+}
+
 // Online-softmax state of one wave over NT tiles of 16 query rows.
 template <int D, int NT>
 struct WaveState {
@@ -181,7 +242,7 @@ struct WaveState {
 };
 
 // Q rows of tile t: global row r = row0 + 16t + n, valid when r < R.
-template <int D, int NT>
+template <int D, int NT, bool KV8 = false>
 __device__ __forceinline__ void load_q(WaveState<D, NT>& s, const PAParams& p, int64_t q_start, int R, int row0,
                                        int kvh, int64_t ctx, int64_t kv_total) {
   const int lane = threadIdx.x & 63;
@@ -198,9 +259,13 @@ __device__ __forceinline__ void load_q(WaveState<D, NT>& s, const PAParams& p, i
     for (int i = 0; i < D / 16; ++i) s.acc[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (r < R) {
       const int qi = r / p.G, g = r % p.G;
-      const uint16_t* qp = q + (q_start + qi) * p.q_ts + (int64_t)(kvh * p.G + g) * p.q_hs + 8 * j;
+      const uint16_t* qp = q + (q_start + qi) * p.q_ts + (int64_t)(kvh * p.G + g) * p.q_hs;
 #pragma unroll
-      for (int c = 0; c < D / 32; ++c) s.q[t][c] = *(const u32x4*)(qp + 32 * c);
+      for (int c = 0; c < D / 32; ++c) {
+        // operand c holds d = 32c + 8j .. +7, or with an E4M3 cache 64(c / 2) + 16j + 8(c % 2) .. +7
+        const int d0 = KV8 ? 64 * (c >> 1) + 16 * j + 8 * (c & 1) : 32 * c + 8 * j;
+        s.q[t][c] = *(const u32x4*)(qp + d0);
+      }
       s.limit[t] = (int)clamp64(ctx + qi + 1, 0, kv_total);
     } else {
 #pragma unroll
@@ -215,20 +280,36 @@ __device__ __forceinline__ void load_q(WaveState<D, NT>& s, const PAParams& p, i
 // LAZY: skip the accumulator rescale when no row max moved (a uniform branch; exact, and a
 // win for decode where the max settles early); otherwise the body is straight-line so the
 // row tiles' dependency chains interleave.
-template <class E, int D, int NT, bool MASKED, bool LAZY = true>
-__device__ __forceinline__ void chunk_scores(WaveState<D, NT>& s, const KRegs<D>& kr, const PAParams& p,
+template <class E, int D, int NT, bool MASKED, bool LAZY = true, class KR>
+__device__ __forceinline__ void chunk_scores(WaveState<D, NT>& s, const KR& kr, const PAParams& p,
                                              const ChunkRef& c, u32x4 pt[NT]) {
   const int j = (threadIdx.x & 63) >> 4;
   f32x4 st[NT][2];
+  if constexpr (std::is_same_v<KR, KRegs<D>>) {
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile) {
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cc = 0; cc < D / 32; ++cc) a = E::mfma(kr.k[tile][cc], s.q[t][cc], a);
+        st[t][tile] = a;
+      }
+  } else {  // E4M3: convert each tile's operands once for all row tiles
 #pragma unroll
     for (int tile = 0; tile < 2; ++tile) {
-      f32x4 a = {0.f, 0.f, 0.f, 0.f};
+      u32x4 k[D / 32];
 #pragma unroll
-      for (int cc = 0; cc < D / 32; ++cc) a = E::mfma(kr.k[tile][cc], s.q[t][cc], a);
-      st[t][tile] = a;
+      for (int cc = 0; cc < D / 32; ++cc) k[cc] = k_operand<E, D>(kr, tile, cc);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cc = 0; cc < D / 32; ++cc) a = E::mfma(k[cc], s.q[t][cc], a);
+        st[t][tile] = a;
+      }
     }
+  }
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     float mx = -INFINITY;
@@ -387,21 +468,61 @@ __device__ __forceinline__ void chunk_pv(WaveState<D, NT>& s, VRegs<D>& vr, cons
   }
 }
 
+// O^T += V^T P^T from an E4M3 V chunk. The A operand of output column group i wants, in dword
+// w, element i of tokens t8 = 2w and 2w + 1; one byte permute gathers that pair for two
+// neighbouring i (bytes b0, b1 of the dwords), and the two halves of the result convert to
+// the two operands' dwords. Masked tokens are zeroed in the raw bytes (E4M3 0x00 is +0).
+template <class E, int D, int NT, bool MASKED>
+__device__ __forceinline__ void chunk_pv(WaveState<D, NT>& s, VRegs8<D>& vr, const ChunkRef& c, int data_end,
+                                         const u32x4 pt[NT]) {
+  constexpr int VW = D / 16;
+  const int j = (threadIdx.x & 63) >> 4;
+  if (MASKED) {
+#pragma unroll
+    for (int t8 = 0; t8 < 8; ++t8) {
+      const int tok = c.tok0 + 16 * (t8 >> 2) + 4 * j + (t8 & 3);
+      const bool keep = c.blk[t8 >> 2] >= 0 && tok < data_end;
+#pragma unroll
+      for (int x = 0; x < VW / 4; ++x) vr.v[t8][x] = keep ? vr.v[t8][x] : 0u;
+    }
+  }
+#pragma unroll
+  for (int x = 0; x < VW / 4; ++x)
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      // bytes 2hb and 2hb + 1 of dword x: elements i0 = 4x + 2hb and i0 + 1
+      const uint32_t sel = hb ? 0x07030602u : 0x05010400u;
+      u32x4 va0, va1;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t pr = __builtin_amdgcn_perm(vr.v[2 * w + 1][x], vr.v[2 * w][x], sel);
+        va0[w] = E::template from_fp8x2<false>(pr);
+        va1[w] = E::template from_fp8x2<true>(pr);
+      }
+      const int i0 = 4 * x + 2 * hb;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        s.acc[t][i0] = E::mfma(va0, pt[t], s.acc[t][i0]);
+        s.acc[t][i0 + 1] = E::mfma(va1, pt[t], s.acc[t][i0 + 1]);
+      }
+    }
+}
+
 // Chunk loop of one wave over tokens tok_begin, tok_begin + stride, ... < tok_hi.
 // The body is straight-line (masks always applied, loads unconditional) and the loads are
 // pinned in the order K(c+1), V(c+1) with scheduling barriers, so each s_waitcnt waits for
 // exactly the operand it guards while the other half of the next chunk stays in flight.
-template <class E, int D, int NT>
+template <class E, int D, int NT, bool KV8 = false>
 __device__ __forceinline__ void run_chunks(WaveState<D, NT>& s, const PAParams& p, const int64_t* btrow, int kvh,
                                            int tok_begin, int stride, int tok_hi, int data_end) {
   if (tok_begin >= tok_hi) return;
   const int page_end = (tok_hi + p.BS - 1) / p.BS;
-  const LaneOffsets lo = lane_offsets<D>(p);
+  const LaneOffsets lo = lane_offsets<D, KV8>(p);
   PageWindow pw;
   load_window(pw, p, btrow, tok_begin / p.BS, page_end);
   ChunkRef c = chunk_ref(pw, p, btrow, tok_begin, tok_hi, page_end);
-  KRegs<D> kr;
-  VRegs<D> vr;
+  std::conditional_t<KV8, KRegs8<D>, KRegs<D>> kr;
+  std::conditional_t<KV8, VRegs8<D>, VRegs<D>> vr;
   load_k<D>(kr, p, c, kvh, lo.k);
   __builtin_amdgcn_sched_barrier(0);
   load_v<D>(vr, p, c, kvh, lo.v);
@@ -490,7 +611,7 @@ __device__ __forceinline__ void write_rows(const WaveState<D, NT>& s, const PAPa
     if (r >= R) continue;
     if (!partial) {
       const int qi = r / p.G, g = r % p.G;
-      const float inv = 1.f / (L == 0.f ? 1.f : L);
+      const float inv = p.v_scale / (L == 0.f ? 1.f : L);
       uint16_t* base = (uint16_t*)p.out + (sv.qs + qi) * p.o_ts + (int64_t)(kvh * p.G + g) * p.o_hs;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -588,17 +709,17 @@ constexpr int kPlanLdsSeqs = 1024;  // flat starts kept in LDS for the unit sear
 __device__ void plan_prefill(const PAParams& p);
 
 // Decode class: grid (NU * HGW / 4) workgroups of 4 waves; wave w of workgroup b is head
-// w % HGW of unit (4 b + w) / HGW. In mixed batches (NUP > 0) workgroup 0 computes the
-// prefill plan instead and the units start at workgroup 1.
-template <class E, int D, int NT>
+// w % HGW of unit (4 b + w) / HGW. In mixed batches (PLAN) workgroup 0 computes the prefill
+// plan instead and the units start at workgroup 1. KV8: the cache is E4M3.
+template <class E, int D, int NT, bool KV8>
 __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
-  if (p.NUP > 0 && blockIdx.x == 0) {
+  if (p.PLAN && blockIdx.x == 0) {
     plan_prefill(p);
     return;
   }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int gw = (blockIdx.x - (p.NUP > 0 ? 1 : 0)) * kWavesPerWG + wave;
+  const int gw = (blockIdx.x - (p.PLAN ? 1 : 0)) * kWavesPerWG + wave;
   const int unit = gw / p.HGW, hw = gw % p.HGW;
   const int NHG = p.Hkv / p.HGW;
 
@@ -644,9 +765,9 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
     const int tok_lo = (int)(pos - seg_beg) * kChunk;
     const int tok_hi = min((int)(y - seg_beg) * kChunk, sv.kv_total);
     WaveState<D, NT> st;
-    load_q<D, NT>(st, p, sv.qs, R, 0, kvh, sv.ctx, sv.kv_total);
+    load_q<D, NT, KV8>(st, p, sv.qs, R, 0, kvh, sv.ctx, sv.kv_total);
     const int64_t* btrow = p.bt + (int64_t)seq * p.bt_rs;
-    run_chunks<E, D, NT>(st, p, btrow, kvh, tok_lo, kChunk, tok_hi, sv.kv_total);
+    run_chunks<E, D, NT, KV8>(st, p, btrow, kvh, tok_lo, kChunk, tok_hi, sv.kv_total);
     const bool whole = pos == seg_beg && y == seg_end;
     const int64_t slot = (int64_t)seq * NHG + hg + unit;
     write_rows<E, D, NT>(st, p, sv, R, 0, kvh, !whole, p.ws_acc, p.ws_ml, (slot * p.HGW + hw) * p.RS);
@@ -749,7 +870,7 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
       for (int f = 0; f < F; ++f) o[f] += s_w[qc[f] / Q4][k] * *(const f32x4*)(src + 4 * qc[f]);
     }
   }
-  if (t < nr) s_inv[t] = 1.f / (L == 0.f ? 1.f : L);
+  if (t < nr) s_inv[t] = p.v_scale / (L == 0.f ? 1.f : L);
   __syncthreads();
 #pragma unroll
   for (int f = 0; f < F; ++f) {
@@ -1049,7 +1170,7 @@ __device__ __forceinline__ void pf_write_rows(const WaveState<D, NT>& s, const P
     if (r >= R) continue;
     if (!partial) {
       const int qi = r / p.G, g = r % p.G;
-      const float inv = 1.f / (L == 0.f ? 1.f : L);
+      const float inv = p.v_scale / (L == 0.f ? 1.f : L);
       uint16_t* base = (uint16_t*)p.out + (sv.qs + qi) * p.o_ts + (int64_t)(kvh * p.G + g) * p.o_hs + 4 * j;
 #pragma unroll
       for (int i = 0; i < D / 16; ++i)
@@ -1404,6 +1525,34 @@ __global__ __launch_bounds__(256, 3) void pa_prefill_kernel(PAParams p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// Prefill class over an E4M3 cache. The LDS ring of pa_prefill_kernel is filled by direct
+// global->LDS loads, which cannot convert; this kernel instead reuses the decode path's
+// register pipeline (load, convert exactly to 16-bit operands, MFMA) with 64 query rows
+// (NT = 4 tiles) per wave and each wave walking the whole context its rows see. Workgroup
+// (x, kvh, k): its 4 waves take row tiles 4x .. 4x + 3 of kv head kvh of the k-th
+// prefill-class sequence (list and count from the prefill plan); a tile past the sequence's
+// rows, or a k past the count, exits at once. The 4 waves read the same K/V (through L2).
+template <class E, int D>
+__global__ __launch_bounds__(256) void pa_rowtile_kernel(PAParams p) {
+  const int n_pre = (int)uni64(p.ws_plan_hdr[2]);
+  const int k = blockIdx.z;
+  if (k >= n_pre) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kvh = blockIdx.y;
+  const int seq = uni(p.ws_pre_list[k]);
+  const SeqView sv = seq_view_uniform(p, seq);
+  const int R = sv.q_len * p.G;
+  const int row0 = (blockIdx.x * kWavesPerWG + wave) * 64;
+  if (row0 >= R) return;
+  const int last = min(R, row0 + 64) - 1;
+  const int tok_hi = (int)clamp64(sv.ctx + last / p.G + 1, 0, sv.kv_total);
+  WaveState<D, 4> st;
+  load_q<D, 4, true>(st, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
+  run_chunks<E, D, 4, true>(st, p, p.bt + (int64_t)seq * p.bt_rs, kvh, 0, kChunk, tok_hi, sv.kv_total);
+  write_rows<E, D, 4>(st, p, sv, R, row0, kvh, false, nullptr, nullptr, 0);
+}
+
+// ---------------------------------------------------------------------------------------
 // Workgroups of 256 threads one launch of `kernel` can keep resident on the current device
 // (cached per device and kernel).
 static int resident_blocks(const void* kernel) {
@@ -1426,23 +1575,24 @@ static int resident_blocks(const void* kernel) {
   return blocks;
 }
 
-template <class E, int D, int NT>
+template <class E, int D, int NT, bool KV8>
 static int launch_decode_nt(PAParams& p, hipStream_t s) {
-  const void* k = (const void*)&pa_decode_kernel<E, D, NT>;
-  const int plan_wgs = p.NUP > 0 ? 1 : 0;  // workgroup 0 plans the prefill launch
+  const void* k = (const void*)&pa_decode_kernel<E, D, NT, KV8>;
+  const int plan_wgs = p.PLAN ? 1 : 0;  // workgroup 0 plans the prefill launch
   int waves = (resident_blocks(k) - plan_wgs) * kWavesPerWG;
   if (waves > kMaxDecodeWaves) waves = kMaxDecodeWaves;
   if (waves < kWavesPerWG) waves = kWavesPerWG;
   p.NU = waves / p.HGW;
   const int wgs = (p.NU * p.HGW + kWavesPerWG - 1) / kWavesPerWG;
-  hipLaunchKernelGGL((pa_decode_kernel<E, D, NT>), dim3(wgs + plan_wgs), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((pa_decode_kernel<E, D, NT, KV8>), dim3(wgs + plan_wgs), dim3(256), 0, s, p);
   return (int)hipGetLastError();
 }
 
-template <class E, int D>
-static int launch_mfma_typed(PAParams& p, const Plan& plan, hipStream_t s, LaunchLog& log) {
+template <class E, int D, bool KV8>
+static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipStream_t s, LaunchLog& log) {
   int err = 0;
-  if (plan.launch_prefill) {
+  p.PLAN = plan.launch_prefill ? 1 : 0;
+  if (plan.launch_prefill && !KV8) {
     // the unit count is fixed before the decode launch: both kernels write merge jobs
     int units = resident_blocks((const void*)&pa_prefill_kernel<E, D>);
     if (units > kMaxPrefillUnits) units = kMaxPrefillUnits;
@@ -1450,16 +1600,25 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, hipStream_t s, Launc
     if (p.NUP < 8) p.NUP = 8;
   }
   switch (plan.NT) {
-    case 1: err = launch_decode_nt<E, D, 1>(p, s); break;
-    case 2: err = launch_decode_nt<E, D, 2>(p, s); break;
-    case 3: err = launch_decode_nt<E, D, 3>(p, s); break;
-    case 4: err = launch_decode_nt<E, D, 4>(p, s); break;
+    case 1: err = launch_decode_nt<E, D, 1, KV8>(p, s); break;
+    case 2: err = launch_decode_nt<E, D, 2, KV8>(p, s); break;
+    case 3: err = launch_decode_nt<E, D, 3, KV8>(p, s); break;
+    case 4: err = launch_decode_nt<E, D, 4, KV8>(p, s); break;
     default: return (int)hipErrorInvalidValue;
   }
   if (err) return err;
   log.after_launch(1, s);
   if (plan.launch_prefill) {
-    hipLaunchKernelGGL((pa_prefill_kernel<E, D>), dim3(p.NUP), dim3(256), 0, s, p);
+    if constexpr (KV8) {
+      // prefill-class sequences have q_len > QS, so at most T / (QS + 1) of them
+      const int tiles = (int)(((int64_t)max_q * p.G + 63) / 64);
+      const int64_t most = p.T / (p.QS + 1);
+      const int seqs = (int)(most < p.B ? (most > 0 ? most : 1) : p.B);
+      const dim3 grid((unsigned)((tiles + kWavesPerWG - 1) / kWavesPerWG), (unsigned)p.Hkv, (unsigned)seqs);
+      hipLaunchKernelGGL((pa_rowtile_kernel<E, D>), grid, dim3(256), 0, s, p);
+    } else {
+      hipLaunchKernelGGL((pa_prefill_kernel<E, D>), dim3(p.NUP), dim3(256), 0, s, p);
+    }
     if ((err = (int)hipGetLastError())) return err;
     log.after_launch(2, s);
   }
@@ -1471,13 +1630,23 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, hipStream_t s, Launc
   return 0;
 }
 
-int launch_paged_attention_mfma(PAParams& p, const Plan& plan, int32_t D, int32_t dtype, hipStream_t s,
-                                LaunchLog& log) {
+template <bool KV8>
+static int launch_mfma_kv(PAParams& p, const Plan& plan, int32_t D, int32_t dtype, int32_t max_q, hipStream_t s,
+                          LaunchLog& log) {
   const bool bf = dtype == 2;
   if (D == 128)
-    return bf ? launch_mfma_typed<BF16, 128>(p, plan, s, log) : launch_mfma_typed<F16, 128>(p, plan, s, log);
-  if (D == 64) return bf ? launch_mfma_typed<BF16, 64>(p, plan, s, log) : launch_mfma_typed<F16, 64>(p, plan, s, log);
+    return bf ? launch_mfma_typed<BF16, 128, KV8>(p, plan, max_q, s, log)
+              : launch_mfma_typed<F16, 128, KV8>(p, plan, max_q, s, log);
+  if (D == 64)
+    return bf ? launch_mfma_typed<BF16, 64, KV8>(p, plan, max_q, s, log)
+              : launch_mfma_typed<F16, 64, KV8>(p, plan, max_q, s, log);
   return (int)hipErrorInvalidValue;
+}
+
+int launch_paged_attention_mfma(PAParams& p, const Plan& plan, int32_t D, int32_t dtype, bool kv8, int32_t max_q,
+                                hipStream_t s, LaunchLog& log) {
+  return kv8 ? launch_mfma_kv<true>(p, plan, D, dtype, max_q, s, log)
+             : launch_mfma_kv<false>(p, plan, D, dtype, max_q, s, log);
 }
 
 }  // namespace kvh

@@ -49,6 +49,72 @@ __global__ __launch_bounds__(256) void reshape_and_cache_kernel(
   }
 }
 
+// FP8 cache (kvh_reshape_and_cache_fp8): the same scatter, each element stored as
+// e4m3(clamp(x / scale, -448, 448)) (fp8_prep / fp8_pack4). A thread converts 8 consecutive
+// elements of one (token, head) row: one 16-byte load (two for fp32 sources), one 8-byte store.
+template <int DT>  // source type: 0 fp32, 1 fp16, 2 bf16
+__global__ __launch_bounds__(256) void reshape_and_cache_fp8_kernel(
+    const uint8_t* k, int64_t k_ts, int64_t k_hs, const uint8_t* v, int64_t v_ts, int64_t v_hs, uint8_t* kc,
+    int64_t k_sb, int64_t k_ss, int64_t k_sh, uint8_t* vc, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+    const int64_t* slots, int64_t num_slots, int Hkv, int D, int BS, float k_scale, float v_scale) {
+  constexpr int EB = DT == 0 ? 4 : 2;
+  const int64_t t = blockIdx.x;
+  const int vpr = D / 8;
+  const int per_tensor = Hkv * vpr;
+  const int idx = blockIdx.y * 256 + threadIdx.x;
+  if (idx >= 2 * per_tensor) return;
+  const int64_t slot = slots[t];
+  if (slot < 0 || slot >= num_slots) return;
+  const int64_t blk = slot / BS, off = slot % BS;
+  const bool is_v = idx >= per_tensor;
+  const int r = is_v ? idx - per_tensor : idx;
+  const int h = r / vpr, x = (r % vpr) * 8;
+  const uint8_t* src = is_v ? v + (t * v_ts + (int64_t)h * v_hs + x) * EB : k + (t * k_ts + (int64_t)h * k_hs + x) * EB;
+  uint8_t* dst = is_v ? vc + blk * v_sb + off * v_ss + (int64_t)h * v_sh + x : kc + blk * k_sb + off * k_ss + (int64_t)h * k_sh + x;
+  const float scale = is_v ? v_scale : k_scale;
+  float f[8];
+  if constexpr (DT == 0) {
+    const f32x4 a = *(const f32x4*)src, b = *(const f32x4*)(src + 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[i] = a[i];
+      f[4 + i] = b[i];
+    }
+  } else {
+    const u32x4 w = *(const u32x4*)src;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint16_t e = (uint16_t)(w[i / 2] >> (16 * (i & 1)));
+      f[i] = DT == 2 ? BF16::to_f32(e) : F16::to_f32(e);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = fp8_prep(f[i], scale);
+  *(u32x2*)dst = u32x2{fp8_pack4(f[0], f[1], f[2], f[3]), fp8_pack4(f[4], f[5], f[6], f[7])};
+}
+
+int launch_reshape_and_cache_fp8(const void* k, int64_t k_ts, int64_t k_hs, const void* v, int64_t v_ts,
+                                 int64_t v_hs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs,
+                                 const int64_t* slots, int64_t T, int64_t num_blocks, int32_t Hkv, int32_t D,
+                                 int32_t BS, int32_t dtype, float k_scale, float v_scale, hipStream_t s) {
+  if (T == 0) return 0;
+  const int total = 2 * Hkv * (D / 8);
+  dim3 grid((unsigned)T, (unsigned)((total + 255) / 256));
+  const int64_t num_slots = num_blocks * BS;
+#define KVH_LAUNCH_RAC8(DT)                                                                                        \
+  hipLaunchKernelGGL((reshape_and_cache_fp8_kernel<DT>), grid, dim3(256), 0, s, (const uint8_t*)k, k_ts, k_hs,    \
+                     (const uint8_t*)v, v_ts, v_hs, (uint8_t*)kc, kcs[0], kcs[1], kcs[2], (uint8_t*)vc, vcs[0],     \
+                     vcs[1], vcs[2], slots, num_slots, Hkv, D, BS, k_scale, v_scale)
+  if (dtype == 2)
+    KVH_LAUNCH_RAC8(2);
+  else if (dtype == 1)
+    KVH_LAUNCH_RAC8(1);
+  else
+    KVH_LAUNCH_RAC8(0);
+#undef KVH_LAUNCH_RAC8
+  return (int)hipGetLastError();
+}
+
 int launch_reshape_and_cache(const void* k, int64_t k_ts, int64_t k_hs, const void* v, int64_t v_ts,
                              int64_t v_hs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs,
                              const int64_t* slots, int64_t T, int64_t num_blocks, int32_t Hkv, int32_t D,

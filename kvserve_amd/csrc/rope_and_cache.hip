@@ -68,15 +68,30 @@ struct RopeElem {
   }
 };
 
-template <int DT>
+// V values (8, or 4 for fp32) prepared for E4M3 and stored as V bytes.
+template <int V>
+__device__ __forceinline__ void store_fp8(uint8_t* dst, const float (&x)[V], float scale) {
+  float y[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) y[i] = fp8_prep(x[i], scale);
+  if constexpr (V == 8)
+    *(u32x2*)dst = u32x2{fp8_pack4(y[0], y[1], y[2], y[3]), fp8_pack4(y[4], y[5], y[6], y[7])};
+  else
+    *(uint32_t*)dst = fp8_pack4(y[0], y[1], y[2], y[3]);
+}
+
+// KV8: the cache is E4M3 (kvh_rope_and_cache_fp8): the rotated keys, rounded to the storage
+// type as above, and the values are then stored as e4m3(clamp(x / scale, -448, 448)).
+template <int DT, bool KV8>
 __global__ __launch_bounds__(256) void rope_and_cache_kernel(
     const uint8_t* qkv, int64_t qkv_ts, const int64_t* positions, const float* cos_t, const float* sin_t,
     int64_t max_pos, uint8_t* q_out, int64_t q_ts, int64_t q_hs, uint8_t* kc, int64_t k_sb, int64_t k_ss,
     int64_t k_sh, uint8_t* vc, int64_t v_sb, int64_t v_ss, int64_t v_sh, const int64_t* slots, int64_t num_slots,
-    int H, int Hkv, int D, int BS) {
+    int H, int Hkv, int D, int BS, float k_scale, float v_scale) {
   using R = RopeElem<DT>;
   constexpr int V = R::kVec;
   constexpr int EB = R::kBytes;
+  constexpr int CB = KV8 ? 1 : EB;  // bytes per cache element
   const int64_t t = blockIdx.x;
   const int half = D / 2;
   const int pv = half / V;  // vectors per half row
@@ -104,21 +119,34 @@ __global__ __launch_bounds__(256) void rope_and_cache_kernel(
         o_lo[j] = R::add(R::mul(lo[j], c_lo), R::mul(-hi[j], s_lo));
         o_hi[j] = R::add(R::mul(hi[j], c_hi), R::mul(lo[j], s_hi));
       }
-      uint8_t* dst;
       if (h < H) {
-        dst = q_out + (t * q_ts + (int64_t)h * q_hs + d) * EB;
+        uint8_t* dst = q_out + (t * q_ts + (int64_t)h * q_hs + d) * EB;
+        R::store(dst, o_lo);
+        R::store(dst + half * EB, o_hi);
       } else {
         if (!in_pool) continue;
-        dst = kc + (blk * k_sb + off * k_ss + (int64_t)(h - H) * k_sh + d) * EB;
+        uint8_t* dst = kc + (blk * k_sb + off * k_ss + (int64_t)(h - H) * k_sh + d) * CB;
+        if constexpr (KV8) {
+          store_fp8<V>(dst, o_lo, k_scale);
+          store_fp8<V>(dst + half, o_hi, k_scale);
+        } else {
+          R::store(dst, o_lo);
+          R::store(dst + half * EB, o_hi);
+        }
       }
-      R::store(dst, o_lo);
-      R::store(dst + half * EB, o_hi);
     } else {
       if (!in_pool) continue;
       const int r = it - n_rot;
       const int h = r / (D / V), d = (r % (D / V)) * V;
-      *(u32x4*)(vc + (blk * v_sb + off * v_ss + (int64_t)h * v_sh + d) * EB) =
-          *(const u32x4*)(row + ((int64_t)(H + Hkv + h) * D + d) * EB);
+      const uint8_t* src = row + ((int64_t)(H + Hkv + h) * D + d) * EB;
+      uint8_t* dst = vc + (blk * v_sb + off * v_ss + (int64_t)h * v_sh + d) * CB;
+      if constexpr (KV8) {
+        float x[V];
+        R::load(src, x);
+        store_fp8<V>(dst, x, v_scale);
+      } else {
+        *(u32x4*)dst = *(const u32x4*)src;
+      }
     }
   }
 }
@@ -127,19 +155,21 @@ int launch_rope_and_cache(const void* qkv, int64_t qkv_ts, const int64_t* positi
                           const float* sin_t, int64_t max_pos, void* q_out, int64_t q_ts, int64_t q_hs, void* kc,
                           const int64_t* kcs, void* vc, const int64_t* vcs, const int64_t* slots, int64_t T,
                           int64_t num_blocks, int32_t H, int32_t Hkv, int32_t D, int32_t BS, int32_t dtype,
-                          hipStream_t s) {
+                          bool kv8, float k_scale, float v_scale, hipStream_t s) {
   if (T == 0) return 0;
   const int64_t num_slots = num_blocks * BS;
-#define KVH_LAUNCH_ROPE(DT)                                                                                      \
-  hipLaunchKernelGGL((rope_and_cache_kernel<DT>), dim3((unsigned)T), dim3(256), 0, s, (const uint8_t*)qkv,      \
-                     qkv_ts, positions, cos_t, sin_t, max_pos, (uint8_t*)q_out, q_ts, q_hs, (uint8_t*)kc, kcs[0], \
-                     kcs[1], kcs[2], (uint8_t*)vc, vcs[0], vcs[1], vcs[2], slots, num_slots, H, Hkv, D, BS)
-  if (dtype == 2)
-    KVH_LAUNCH_ROPE(2);
-  else if (dtype == 1)
-    KVH_LAUNCH_ROPE(1);
-  else
-    KVH_LAUNCH_ROPE(0);
+#define KVH_LAUNCH_ROPE(DT, KV8)                                                                                  \
+  hipLaunchKernelGGL((rope_and_cache_kernel<DT, KV8>), dim3((unsigned)T), dim3(256), 0, s, (const uint8_t*)qkv,  \
+                     qkv_ts, positions, cos_t, sin_t, max_pos, (uint8_t*)q_out, q_ts, q_hs, (uint8_t*)kc, kcs[0],  \
+                     kcs[1], kcs[2], (uint8_t*)vc, vcs[0], vcs[1], vcs[2], slots, num_slots, H, Hkv, D, BS,        \
+                     k_scale, v_scale)
+  if (dtype == 2) {
+    if (kv8) KVH_LAUNCH_ROPE(2, true); else KVH_LAUNCH_ROPE(2, false);
+  } else if (dtype == 1) {
+    if (kv8) KVH_LAUNCH_ROPE(1, true); else KVH_LAUNCH_ROPE(1, false);
+  } else {
+    if (kv8) KVH_LAUNCH_ROPE(0, true); else KVH_LAUNCH_ROPE(0, false);
+  }
 #undef KVH_LAUNCH_ROPE
   return (int)hipGetLastError();
 }

@@ -85,6 +85,11 @@ class Attention(nn.Module):
         self.qkv_proj = nn.Linear(cfg.hidden_size, self.q_size + 2 * self.kv_size, bias=False)
         self.o_proj = nn.Linear(self.q_size, cfg.hidden_size, bias=False)
         self.scale = self.head_dim**-0.5
+        # per-layer scales of a float8_e4m3fn KV cache (unused for 16-bit caches)
+        self.k_scale = self.v_scale = 1.0
+
+    def _kv_scales(self, cache: torch.Tensor) -> dict:
+        return {"k_scale": self.k_scale, "v_scale": self.v_scale} if cache.dtype == torch.float8_e4m3fn else {}
 
     def project(self, x: torch.Tensor, positions: torch.Tensor, rope: RotaryEmbedding):
         """[T, hidden] -> q [T, H, D], k [T, Hkv, D] (RoPE applied), v [T, Hkv, D] (a strided
@@ -100,17 +105,19 @@ class Attention(nn.Module):
     def attend(self, q, k, v, kv_cache: torch.Tensor, meta: AttentionMetadata, out: torch.Tensor | None = None):
         """Write this step's K/V into the paged cache and attend over it (model.py:96-108)."""
         k_cache, v_cache = kv_cache[0], kv_cache[1]
-        self.backend.write_kv(k_cache, v_cache, k, v, meta.slot_mapping)
-        return self.backend.forward(q, k_cache, v_cache, meta, self.scale, out=out)
+        sc = self._kv_scales(k_cache)
+        self.backend.write_kv(k_cache, v_cache, k, v, meta.slot_mapping, **sc)
+        return self.backend.forward(q, k_cache, v_cache, meta, self.scale, out=out, **sc)
 
     def attend_fused(self, qkv, positions, rope: RotaryEmbedding, kv_cache: torch.Tensor, meta: AttentionMetadata,
                      out: torch.Tensor | None = None):  # fmt: skip
         """RoPE, QKV split and the cache write in the backend's one kernel, then attention: the
         same result as project() + attend() (bit for bit) with the RoPE moved out of the piece."""
         k_cache, v_cache = kv_cache[0], kv_cache[1]
+        sc = self._kv_scales(k_cache)
         q = self.backend.rope_and_cache(qkv, positions, rope.cos, rope.sin, k_cache, v_cache, meta.slot_mapping,
-                                        self.num_heads)  # fmt: skip
-        return self.backend.forward(q, k_cache, v_cache, meta, self.scale, out=out)
+                                        self.num_heads, **sc)  # fmt: skip
+        return self.backend.forward(q, k_cache, v_cache, meta, self.scale, out=out, **sc)
 
 
 class MLP(nn.Module):

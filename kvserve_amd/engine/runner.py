@@ -152,7 +152,8 @@ class ModelRunner:
 
     def __init__(self, model, num_blocks: int, block_size: int = 16, max_model_len: int = 4096,
                  use_graphs: bool = True, max_graph_batch: int = 128, prefill_token_budget: int = 2048,
-                 device_metadata: bool | None = None, max_seqs: int = 1024):  # fmt: skip
+                 device_metadata: bool | None = None, max_seqs: int = 1024,
+                 kv_cache_dtype: torch.dtype | None = None):  # fmt: skip
         cfg = model.cfg
         p = next(model.parameters())
         self.model = model
@@ -161,8 +162,14 @@ class ModelRunner:
         self.max_model_len = max_model_len
         self.num_blocks = num_blocks
         self.scratch_block = num_blocks
-        self.kv_caches = torch.zeros(cfg.num_layers, 2, num_blocks + 1, block_size, cfg.num_kv_heads, cfg.head_dim,
-                                     dtype=self.dtype, device=self.device)  # fmt: skip
+        # kv_cache_dtype: the model's dtype, or torch.float8_e4m3fn (E4M3 with each layer's
+        # k_scale / v_scale; HIP backend only)
+        self.kv_dtype = self.dtype if kv_cache_dtype is None else kv_cache_dtype
+        shape = (cfg.num_layers, 2, num_blocks + 1, block_size, cfg.num_kv_heads, cfg.head_dim)
+        if self.kv_dtype == torch.float8_e4m3fn:  # zero bytes, viewed as E4M3 (+0)
+            self.kv_caches = torch.zeros(shape, dtype=torch.uint8, device=self.device).view(self.kv_dtype)
+        else:
+            self.kv_caches = torch.zeros(shape, dtype=self.kv_dtype, device=self.device)
         self.free_blocks = list(range(num_blocks - 1, -1, -1))
         self.prefill_token_budget = prefill_token_budget
         backend = model.layers[0].self_attn.backend

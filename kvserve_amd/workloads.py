@@ -83,12 +83,14 @@ class Workload:
         n = self.unique_tokens() if unique else sum(self.seq_lens)
         return 2 * self.num_kv_heads * self.head_dim * elem_bytes * n
 
-    def algorithmic_bytes(self, elem_bytes: int, unique: bool = True) -> int:
-        """K/V read once + Q read + O written + block-table and length metadata."""
+    def algorithmic_bytes(self, elem_bytes: int, unique: bool = True, kv_elem_bytes: int | None = None) -> int:
+        """K/V read once + Q read + O written + block-table and length metadata (K/V elements
+        of kv_elem_bytes, 1 for an E4M3 cache; default elem_bytes)."""
         qo = 2 * self.num_tokens * self.num_heads * self.head_dim * elem_bytes
         bt = 8 * sum(math.ceil(s / self.block_size) for s in self.seq_lens)
         md = 8 * (3 * len(self.seq_lens) + 1)
-        return self.kv_bytes(elem_bytes, unique) + qo + bt + md
+        kv = self.kv_bytes(elem_bytes if kv_elem_bytes is None else kv_elem_bytes, unique)
+        return kv + qo + bt + md
 
     def flops(self) -> int:
         """4 * H * D per visible (query row, key) pair: QK^T and PV, multiply-add = 2."""

@@ -12,7 +12,7 @@ from kvserve_amd import HipAttention
 from kvserve_amd.engine import LLAMA_3_2_1B, ModelConfig
 from kvserve_amd.engine.model import build_model
 from kvserve_amd.engine.runner import ModelRunner, Sequence
-from tests.engine_backends import TorchRefAttention
+from tests.engine_backends import TorchRefAttention, TorchRefFP8Attention
 
 pytestmark = pytest.mark.gpu
 
@@ -110,3 +110,49 @@ def test_device_metadata_runner_matches_host_metadata_runner(hip_device):
         out[dev_meta] = [r.generate(PROMPTS, max_new_tokens=12), r.generate(PROMPTS[::-1], max_new_tokens=12)]
         assert r.steps["decode_graph"] == 22
     assert out[True] == out[False]
+
+
+def test_fp8_kv_cache_matches_torch_over_the_same_cache_and_graphs_match_eager(hip_device):
+    """A bf16 model over an E4M3 KV cache (scales 0.5 / 0.25): the HIP backend's prefill logits
+    match the torch backend's over the same E4M3 cache (write: the oracle's quantization;
+    attention: fp32 over the dequantized cache) within 5% of the logit scale, as the bf16 test
+    above, and decode steps replayed from HIP graphs give the eager steps' logits (3%: the graph
+    pads the batch, so the GEMMs may differ)."""
+
+    def with_scales(model):
+        for layer in model.layers:
+            layer.self_attn.k_scale, layer.self_attn.v_scale = 0.5, 0.25
+        return model
+
+    logits = {}
+    for name, backend in (("hip", HipAttention), ("torch", TorchRefFP8Attention)):
+        r = ModelRunner(with_scales(_model(backend, torch.bfloat16)), num_blocks=128, max_model_len=1024,
+                        use_graphs=False, kv_cache_dtype=torch.float8_e4m3fn)  # fmt: skip
+        seqs = [Sequence(list(p)) for p in PROMPTS]
+        captured = {}
+        orig = r.model.compute_logits
+        r.model.compute_logits = lambda h, _o=orig, _c=captured: _c.setdefault("l", _o(h))
+        r.prefill(seqs)
+        logits[name] = captured["l"]
+    scale = logits["torch"].abs().max().item()
+    assert (logits["hip"] - logits["torch"]).abs().max().item() <= 0.05 * scale
+    runners = [
+        ModelRunner(with_scales(_model(HipAttention, torch.bfloat16)), num_blocks=128, max_model_len=1024,
+                    use_graphs=g, max_graph_batch=8, kv_cache_dtype=torch.float8_e4m3fn)
+        for g in (True, False)
+    ]  # fmt: skip
+    seqs = [[Sequence(list(p)) for p in PROMPTS[:3]] for _ in runners]
+    for r, s in zip(runners, seqs):
+        r.prefill(s)
+    for step in range(4):
+        outs = []
+        for r, s in zip(runners, seqs):
+            captured = {}
+            orig = r.model.compute_logits
+            r.model.compute_logits = lambda h, _o=orig, _c=captured: _c.setdefault("l", _o(h))
+            r.decode(s)
+            r.model.compute_logits = orig
+            outs.append(captured["l"])
+        diff = (outs[0] - outs[1]).abs().max().item()
+        assert diff <= 3e-2 * outs[1].abs().max().item(), (step, diff)
+    assert runners[0].steps["decode_graph"] == 4
