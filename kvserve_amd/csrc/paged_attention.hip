@@ -1527,13 +1527,18 @@ __global__ __launch_bounds__(256, 3) void pa_prefill_kernel(PAParams p) {
 // ---------------------------------------------------------------------------------------
 // Prefill class over an E4M3 cache. The LDS ring of pa_prefill_kernel is filled by direct
 // global->LDS loads, which cannot convert; this kernel instead reuses the decode path's
-// register pipeline (load, convert exactly to 16-bit operands, MFMA) with 64 query rows
-// (NT = 4 tiles) per wave and each wave walking the whole context its rows see. Workgroup
+// register pipeline (load, convert exactly to 16-bit operands, MFMA) with 16 kRowTileNT
+// query rows per wave and each wave walking the whole context its rows see. Workgroup
 // (x, kvh, k): its 4 waves take row tiles 4x .. 4x + 3 of kv head kvh of the k-th
 // prefill-class sequence (list and count from the prefill plan); a tile past the sequence's
 // rows, or a k past the count, exits at once. The 4 waves read the same K/V (through L2).
+// Measured at C3: 16 rows per wave 115 us, 32 rows 120 us, 64 rows 167 us (more waves
+// resident beat fewer K/V re-reads).
+constexpr int kRowTileNT = 1;  // 16-row tiles per wave of pa_rowtile_kernel (1: most waves, measured best)
+
 template <class E, int D>
 __global__ __launch_bounds__(256) void pa_rowtile_kernel(PAParams p) {
+  constexpr int NT = kRowTileNT, RW = 16 * NT;  // rows per wave
   const int n_pre = (int)uni64(p.ws_plan_hdr[2]);
   const int k = blockIdx.z;
   if (k >= n_pre) return;
@@ -1542,14 +1547,14 @@ __global__ __launch_bounds__(256) void pa_rowtile_kernel(PAParams p) {
   const int seq = uni(p.ws_pre_list[k]);
   const SeqView sv = seq_view_uniform(p, seq);
   const int R = sv.q_len * p.G;
-  const int row0 = (blockIdx.x * kWavesPerWG + wave) * 64;
+  const int row0 = (blockIdx.x * kWavesPerWG + wave) * RW;
   if (row0 >= R) return;
-  const int last = min(R, row0 + 64) - 1;
+  const int last = min(R, row0 + RW) - 1;
   const int tok_hi = (int)clamp64(sv.ctx + last / p.G + 1, 0, sv.kv_total);
-  WaveState<D, 4> st;
-  load_q<D, 4, true>(st, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
-  run_chunks<E, D, 4, true>(st, p, p.bt + (int64_t)seq * p.bt_rs, kvh, 0, kChunk, tok_hi, sv.kv_total);
-  write_rows<E, D, 4>(st, p, sv, R, row0, kvh, false, nullptr, nullptr, 0);
+  WaveState<D, NT> st;
+  load_q<D, NT, true>(st, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
+  run_chunks<E, D, NT, true>(st, p, p.bt + (int64_t)seq * p.bt_rs, kvh, 0, kChunk, tok_hi, sv.kv_total);
+  write_rows<E, D, NT>(st, p, sv, R, row0, kvh, false, nullptr, nullptr, 0);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1611,7 +1616,7 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipSt
   if (plan.launch_prefill) {
     if constexpr (KV8) {
       // prefill-class sequences have q_len > QS, so at most T / (QS + 1) of them
-      const int tiles = (int)(((int64_t)max_q * p.G + 63) / 64);
+      const int tiles = (int)(((int64_t)max_q * p.G + 16 * kRowTileNT - 1) / (16 * kRowTileNT));
       const int64_t most = p.T / (p.QS + 1);
       const int seqs = (int)(most < p.B ? (most > 0 ? most : 1) : p.B);
       const dim3 grid((unsigned)((tiles + kWavesPerWG - 1) / kWavesPerWG), (unsigned)p.Hkv, (unsigned)seqs);
