@@ -2,6 +2,7 @@
 """Benchmark of the HIP paged-attention backend on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-secondary]
+    python bench.py --only N [--fp8]      # one BASELINE config (E4M3 KV caches with --fp8)
 
 Headline workload: BASELINE config 2 (Llama-3.1-8B decode layer: 64 sequences, 32 q / 8 kv
 heads, head_dim 128, block 16, contexts U[1024, 8192], bf16), the config the metric is
@@ -418,6 +419,7 @@ def main() -> int:
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", type=int, default=0, help="run just this config (1-5) and print its record")
+    p.add_argument("--fp8", action="store_true", help="with --only: E4M3 KV caches")
     p.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
     p.add_argument("--no-engine", action="store_true", help="skip the 1B/8B engine decode tokens/s")
     p.add_argument("--engine-only", action="store_true", help="run just the engine decode tokens/s")
@@ -445,7 +447,7 @@ def main() -> int:
         return 1
 
     if args.only:
-        print(json.dumps(measure(args.only, args.steps, args.warmup, args.prof_iters)), flush=True)
+        print(json.dumps(measure(args.only, args.steps, args.warmup, args.prof_iters, fp8=args.fp8)), flush=True)
         return 0
     engine_batches = {"llama_3_2_1b": [1, 8, 32, 64, 128], "llama_3_1_8b": [1, 8, 32, 64]}
     if args.engine_only:
