@@ -1208,7 +1208,7 @@ __device__ __forceinline__ void wait_vm() {
 template <class E, int D>
 __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const SeqView& sv, int R, int seq,
                                              int kvh, int t, int c_lo, int c_hi, int w, bool partial,
-                                             int64_t slot) {
+                                             int64_t slot, int rest, int total) {
   constexpr int NT = kPrefillNQT;
   using L = PrefillLds<D>;
   c_lo = uni(c_lo);
@@ -1264,6 +1264,16 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
 
   // step i: wait for chunk i, then refill the stage chunk i - 1 used (`next`) with chunk i + 2
   auto sync = [&](int i, int next) {
+    // Wave priority from the unit's remaining share of its work (total positions, rest of
+    // them after this tile): the arbiter favours older waves, so workgroups that started
+    // together on a CU drift apart and the last one runs its tail alone; raising the
+    // priority of the workgroups that are behind keeps them together.
+    const int left = rest + (n - i);
+    const int lvl = min(3, (4 * left) / (total + 1));
+    if (lvl >= 2)
+      lvl == 3 ? __builtin_amdgcn_s_setprio(3) : __builtin_amdgcn_s_setprio(2);
+    else
+      lvl == 1 ? __builtin_amdgcn_s_setprio(1) : __builtin_amdgcn_s_setprio(0);
     const int ci2 = c_lo + i + 2;
     if (i + 2 < n && ci2 - win.c0 >= 64) {  // the window moves on (every 62 chunks)
       pf_window(win, p, btrow, c_lo + i, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
@@ -1497,7 +1507,8 @@ __global__ __launch_bounds__(256, 3) void pa_prefill_kernel(PAParams p) {
     if (c_hi > c_lo) {
       const bool whole = c_lo == 0 && c_hi == n_t;
       const int64_t slot = 2 * (int64_t)u + (first ? 0 : 1);
-      prefill_tile<E, D>(lds, p, sv, R, seq, kvh, t, c_lo, c_hi, w, !whole, slot);
+      prefill_tile<E, D>(lds, p, sv, R, seq, kvh, t, c_lo, c_hi, w, !whole, slot, (int)(x1 - (x + (b - a))),
+                         (int)(x1 - (u * C / NUa)));
       if (threadIdx.x == 0 && c_lo == 0 && c_hi < n_t) {
         // the tile continues in units u + 1 .. u1, each holding it as its first piece
         const int64_t x_last = x + (tw - a) - 1;
