@@ -230,6 +230,31 @@ KVH_API int kvh_paged_attention_fp8(const void* q, int64_t q_tok_stride, int64_t
                             void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Engine-harness kernels (no counterpart in the attention path; they serve the Llama layer
+ * around it, src/kvserve/model.py:22-32 and its MLP), fp16 / bf16 rows with 16-byte aligned
+ * pointers and strides that are multiples of 8 elements:
+ *
+ * add_rmsnorm: x' = x + delta rounded to dtype (written to x_out), then
+ *   h_out = weight * (x' * rsqrt(mean(x'^2) + eps)).to(dtype), the statistics in fp32; with
+ *   delta == NULL it is the plain RMSNorm of x (x_out unused). One pass instead of an add and
+ *   seven PyTorch kernels. hidden % 8 == 0.
+ */
+KVH_API int kvh_add_rmsnorm(const void* x, int64_t x_tok_stride, const void* delta, int64_t delta_tok_stride,
+                            const void* weight, void* x_out, int64_t x_out_tok_stride,
+                            void* h_out, int64_t h_tok_stride, int64_t num_tokens, int32_t hidden, float eps,
+                            int32_t dtype, void* stream);
+
+/* silu_mul: out[t] = silu(gate_up[t, :I]).to(dtype) * gate_up[t, I:2I] (the fused gate/up
+ * projection's halves), I = intermediate, I % 8 == 0, num_tokens <= 65535. */
+KVH_API int kvh_silu_mul(const void* gate_up, int64_t gate_up_tok_stride, void* out, int64_t out_tok_stride,
+                         int64_t num_tokens, int32_t intermediate, int32_t dtype, void* stream);
+
+/* gemv: y[i][j] = sum_k x[i][k] * weight[j][k] (nn.Linear, weight [n, k] row-major) for
+ * m <= 8 rows, fp32 accumulation, rounded to dtype; k % 8 == 0. Streams the weight once. */
+KVH_API int kvh_gemv(const void* x, int64_t x_row_stride, const void* weight, int64_t w_row_stride,
+                     void* y, int64_t y_row_stride, int32_t m, int32_t n, int32_t k, int32_t dtype, void* stream);
+
+/*
  * Launch-timing hook for benchmarks (no counterpart in the reference). When armed with an
  * array of n <= 8 hipEvent_t handles (created by the caller with timing enabled), the NEXT
  * kvh_paged_attention call on this host thread records events[0] on its stream before its

@@ -93,6 +93,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _sz, _vp,  # workspace, stream
         ],  # fmt: skip
     ),
+    "kvh_add_rmsnorm": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i32, _f32, _i32, _vp],
+    ),
+    "kvh_silu_mul": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp]),
+    "kvh_gemv": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "kvh_profile_arm": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), _i32]),
     "kvh_last_launch_kernels": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int32), _i32]),
 }

@@ -23,6 +23,7 @@ LIB = LIB_DIR / "libkvhip.so"
 INCLUDE = PKG.parent / "include"
 
 SOURCES = [
+    "engine_ops.hip",
     "kvh_api.hip",
     "metadata.hip",
     "paged_attention.hip",

@@ -1,0 +1,250 @@
+// Engine-harness kernels around the attention path: the elementwise steps of a Llama layer
+// fused into single passes, and a weight-streaming GEMV for decode-sized batches. They serve
+// kvserve_amd.engine (the counterpart of the reference's model.py), not the attention ABI.
+//
+//   add_rmsnorm: x' = x + delta (rounded to the storage type, as PyTorch's add), then
+//                h = weight * (x' * rsqrt(mean(x'^2) + eps)).to(dtype)   (model.py:22-32)
+//                one workgroup per token row; replaces an add and seven norm kernels.
+//   silu_mul:    out = silu(gate).to(dtype) * up (model.py MLP), gate / up the two halves of
+//                the fused gate_up projection; replaces a chunk view, silu and a multiply.
+//   gemv:        y[m][n] = sum_k x[m][k] w[n][k] for m < M <= 8 (nn.Linear with a [N, K]
+//                weight), fp32 accumulation; HBM-bound on the weight, which each wave
+//                streams in 1 KB loads while x comes from L1/L2.
+#include "kvh_device.h"
+#include "kvh_internal.h"
+
+namespace kvh {
+namespace {
+
+constexpr int kOpsThreads = 256;
+
+template <class E>
+__device__ __forceinline__ void unpack8(const u32x4& w, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = E::to_f32((uint16_t)(w[i / 2] >> (16 * (i & 1))));
+}
+
+template <class E>
+__device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
+  return u32x4{E::pack2(f[0], f[1]), E::pack2(f[2], f[3]), E::pack2(f[4], f[5]), E::pack2(f[6], f[7])};
+}
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kOpsThreads / 64; ++i) s += red[i];
+  return s;
+}
+
+template <class E>
+__global__ __launch_bounds__(kOpsThreads) void add_rmsnorm_kernel(const uint16_t* __restrict__ x, int64_t x_ts,
+                                                                  const uint16_t* __restrict__ d, int64_t d_ts,
+                                                                  const uint16_t* __restrict__ w,
+                                                                  uint16_t* __restrict__ xo, int64_t xo_ts,
+                                                                  uint16_t* __restrict__ h, int64_t h_ts, int hd,
+                                                                  float eps) {
+  __shared__ float red[kOpsThreads / 64];
+  const int64_t t = blockIdx.x;
+  const int nv = hd / 8;
+  const uint16_t* xr = x + t * x_ts;
+  uint16_t* xor_ = xo + t * xo_ts;
+  float ss = 0.f;
+  for (int v = threadIdx.x; v < nv; v += kOpsThreads) {
+    float a[8];
+    unpack8<E>(*(const u32x4*)(xr + 8 * v), a);
+    if (d) {
+      float b[8];
+      unpack8<E>(*(const u32x4*)(d + t * d_ts + 8 * v), b);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] += b[i];
+      const u32x4 o = pack8<E>(a);
+      *(u32x4*)(xor_ + 8 * v) = o;
+      unpack8<E>(o, a);  // the rounded sum is what the norm sees
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += a[i] * a[i];
+  }
+  const float r = rsqrtf(block_sum(ss, red) / (float)hd + eps);
+  const uint16_t* src = d ? xor_ : xr;
+  for (int v = threadIdx.x; v < nv; v += kOpsThreads) {
+    float a[8], g[8];
+    unpack8<E>(*(const u32x4*)(src + 8 * v), a);
+    unpack8<E>(*(const u32x4*)(w + 8 * v), g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] *= r;
+    unpack8<E>(pack8<E>(a), a);  // .to(dtype) before the weight
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] *= g[i];
+    *(u32x4*)(h + t * h_ts + 8 * v) = pack8<E>(a);
+  }
+}
+
+template <class E>
+__global__ __launch_bounds__(kOpsThreads) void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t gu_ts,
+                                                               uint16_t* __restrict__ out, int64_t o_ts, int inter) {
+  const int64_t t = blockIdx.y;
+  const int v = blockIdx.x * kOpsThreads + threadIdx.x;
+  if (8 * v >= inter) return;
+  float g[8], u[8];
+  unpack8<E>(*(const u32x4*)(gu + t * gu_ts + 8 * v), g);
+  unpack8<E>(*(const u32x4*)(gu + t * gu_ts + inter + 8 * v), u);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) g[i] = g[i] / (1.f + expf(-g[i]));
+  unpack8<E>(pack8<E>(g), g);  // silu(gate) in the storage type, then the product
+#pragma unroll
+  for (int i = 0; i < 8; ++i) g[i] *= u[i];
+  *(u32x4*)(out + t * o_ts + 8 * v) = pack8<E>(g);
+}
+
+// GEMV: a wave owns RW consecutive weight rows and walks k in steps of 512 (64 lanes x 8
+// elements, one 16-byte load per lane per row), two steps per iteration so 2 RW weight loads
+// are in flight; lane partial sums are reduced across the wave at the end.
+template <class E, int M, int RW>
+__global__ __launch_bounds__(kOpsThreads) void gemv_kernel(const uint16_t* __restrict__ x, int64_t x_rs,
+                                                           const uint16_t* __restrict__ w, int64_t w_rs,
+                                                           uint16_t* __restrict__ y, int64_t y_rs, int n, int k) {
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * (kOpsThreads / 64) + (threadIdx.x >> 6);
+  const int n0 = wave * RW;
+  if (n0 >= n) return;
+  float acc[M][RW];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) acc[m][r] = 0.f;
+  const uint16_t* wr[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) wr[r] = w + (int64_t)min(n0 + r, n - 1) * w_rs;  // rows past n repeat the last
+  const int kfull = k / 1024 * 1024;
+  for (int k0 = 8 * lane; k0 < kfull; k0 += 1024) {
+    u32x4 wv[2][RW], xv[2][M];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+      for (int r = 0; r < RW; ++r) wv[s][r] = *(const u32x4*)(wr[r] + k0 + 512 * s);
+#pragma unroll
+      for (int m = 0; m < M; ++m) xv[s][m] = *(const u32x4*)(x + m * x_rs + k0 + 512 * s);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float xf[8];
+        unpack8<E>(xv[s][m], xf);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          float wf[8];
+          unpack8<E>(wv[s][r], wf);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[m][r] += xf[i] * wf[i];
+        }
+      }
+  }
+  for (int k0 = kfull + 8 * lane; k0 < k; k0 += 512) {  // tail: k % 1024 (k % 8 == 0)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float xf[8];
+      unpack8<E>(*(const u32x4*)(x + m * x_rs + k0), xf);
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        float wf[8];
+        unpack8<E>(*(const u32x4*)(wr[r] + k0), wf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[m][r] += xf[i] * wf[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      float v = acc[m][r];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+      acc[m][r] = v;
+    }
+  if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int r = 0; r < RW; ++r)
+        if (n0 + r < n) y[m * y_rs + n0 + r] = (uint16_t)(E::pack2(acc[m][r], 0.f) & 0xffffu);
+  }
+}
+
+template <class E, int M>
+int launch_gemv_m(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int n, int k,
+                  hipStream_t s) {
+  // rows per wave: enough waves to fill the chip for small n, fewer reductions for large n
+  const int rw = n >= 16384 ? 4 : (n >= 4096 ? 2 : 1);
+  const int waves = (n + rw - 1) / rw;
+  const dim3 grid((waves + kOpsThreads / 64 - 1) / (kOpsThreads / 64));
+  if (rw == 4)
+    hipLaunchKernelGGL((gemv_kernel<E, M, 4>), grid, dim3(kOpsThreads), 0, s, (const uint16_t*)x, x_rs,
+                       (const uint16_t*)w, w_rs, (uint16_t*)y, y_rs, n, k);
+  else if (rw == 2)
+    hipLaunchKernelGGL((gemv_kernel<E, M, 2>), grid, dim3(kOpsThreads), 0, s, (const uint16_t*)x, x_rs,
+                       (const uint16_t*)w, w_rs, (uint16_t*)y, y_rs, n, k);
+  else
+    hipLaunchKernelGGL((gemv_kernel<E, M, 1>), grid, dim3(kOpsThreads), 0, s, (const uint16_t*)x, x_rs,
+                       (const uint16_t*)w, w_rs, (uint16_t*)y, y_rs, n, k);
+  return (int)hipGetLastError();
+}
+
+template <class E>
+int launch_gemv_t(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int m, int n,
+                  int k, hipStream_t s) {
+  switch (m) {
+    case 1: return launch_gemv_m<E, 1>(x, x_rs, w, w_rs, y, y_rs, n, k, s);
+    case 2: return launch_gemv_m<E, 2>(x, x_rs, w, w_rs, y, y_rs, n, k, s);
+    case 3: return launch_gemv_m<E, 3>(x, x_rs, w, w_rs, y, y_rs, n, k, s);
+    case 4: return launch_gemv_m<E, 4>(x, x_rs, w, w_rs, y, y_rs, n, k, s);
+    case 5: return launch_gemv_m<E, 5>(x, x_rs, w, w_rs, y, y_rs, n, k, s);
+    case 6: return launch_gemv_m<E, 6>(x, x_rs, w, w_rs, y, y_rs, n, k, s);
+    case 7: return launch_gemv_m<E, 7>(x, x_rs, w, w_rs, y, y_rs, n, k, s);
+    default: return launch_gemv_m<E, 8>(x, x_rs, w, w_rs, y, y_rs, n, k, s);
+  }
+}
+
+}  // namespace
+
+int launch_add_rmsnorm(const void* x, int64_t x_ts, const void* d, int64_t d_ts, const void* w, void* xo,
+                       int64_t xo_ts, void* h, int64_t h_ts, int64_t T, int32_t hd, float eps, int32_t dtype,
+                       hipStream_t s) {
+  if (T == 0) return 0;
+  if (dtype == 2)
+    hipLaunchKernelGGL((add_rmsnorm_kernel<BF16>), dim3((unsigned)T), dim3(kOpsThreads), 0, s, (const uint16_t*)x,
+                       x_ts, (const uint16_t*)d, d_ts, (const uint16_t*)w, (uint16_t*)xo, xo_ts, (uint16_t*)h, h_ts,
+                       hd, eps);
+  else
+    hipLaunchKernelGGL((add_rmsnorm_kernel<F16>), dim3((unsigned)T), dim3(kOpsThreads), 0, s, (const uint16_t*)x,
+                       x_ts, (const uint16_t*)d, d_ts, (const uint16_t*)w, (uint16_t*)xo, xo_ts, (uint16_t*)h, h_ts,
+                       hd, eps);
+  return (int)hipGetLastError();
+}
+
+int launch_silu_mul(const void* gu, int64_t gu_ts, void* out, int64_t o_ts, int64_t T, int32_t inter, int32_t dtype,
+                    hipStream_t s) {
+  if (T == 0) return 0;
+  const dim3 grid((unsigned)((inter / 8 + kOpsThreads - 1) / kOpsThreads), (unsigned)T);
+  if (dtype == 2)
+    hipLaunchKernelGGL((silu_mul_kernel<BF16>), grid, dim3(kOpsThreads), 0, s, (const uint16_t*)gu, gu_ts,
+                       (uint16_t*)out, o_ts, inter);
+  else
+    hipLaunchKernelGGL((silu_mul_kernel<F16>), grid, dim3(kOpsThreads), 0, s, (const uint16_t*)gu, gu_ts,
+                       (uint16_t*)out, o_ts, inter);
+  return (int)hipGetLastError();
+}
+
+int launch_gemv(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int32_t m, int32_t n,
+                int32_t k, int32_t dtype, hipStream_t s) {
+  return dtype == 2 ? launch_gemv_t<BF16>(x, x_rs, w, w_rs, y, y_rs, m, n, k, s)
+                    : launch_gemv_t<F16>(x, x_rs, w, w_rs, y, y_rs, m, n, k, s);
+}
+
+}  // namespace kvh

@@ -460,6 +460,51 @@ int kvh_paged_attention_fp8(const void* q, int64_t q_tok_stride, int64_t q_head_
                               workspace, workspace_bytes, stream);
 }
 
+static bool a16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int kvh_add_rmsnorm(const void* x, int64_t x_tok_stride, const void* delta, int64_t delta_tok_stride,
+                    const void* weight, void* x_out, int64_t x_out_tok_stride, void* h_out, int64_t h_tok_stride,
+                    int64_t num_tokens, int32_t hidden, float eps, int32_t dtype, void* stream) {
+  if (dtype != KVH_DTYPE_F16 && dtype != KVH_DTYPE_BF16) return KVH_E_DTYPE;
+  if (num_tokens < 0 || num_tokens > 0x7fffffffLL || hidden <= 0 || !(eps >= 0.f)) return KVH_E_SHAPE;
+  if (hidden % 8 != 0) return KVH_E_UNSUPPORTED;
+  if (num_tokens == 0) return KVH_OK;
+  if (!x || !weight || !h_out || (delta && !x_out)) return KVH_E_NULL;
+  const int64_t st[] = {x_tok_stride, h_tok_stride, delta_tok_stride, x_out_tok_stride};
+  for (int i = 0; i < (delta ? 4 : 2); ++i) {  // without delta, x_out and its stride are unused
+    if (st[i] < hidden) return KVH_E_SHAPE;
+    if (st[i] % 8) return KVH_E_ALIGN;
+  }
+  if (!a16(x) || !a16(weight) || !a16(h_out) || (delta && (!a16(delta) || !a16(x_out)))) return KVH_E_ALIGN;
+  return launch_add_rmsnorm(x, x_tok_stride, delta, delta_tok_stride, weight, x_out, x_out_tok_stride, h_out,
+                            h_tok_stride, num_tokens, hidden, eps, dtype, (hipStream_t)stream);
+}
+
+int kvh_silu_mul(const void* gate_up, int64_t gate_up_tok_stride, void* out, int64_t out_tok_stride,
+                 int64_t num_tokens, int32_t intermediate, int32_t dtype, void* stream) {
+  if (dtype != KVH_DTYPE_F16 && dtype != KVH_DTYPE_BF16) return KVH_E_DTYPE;
+  if (num_tokens < 0 || num_tokens > 65535 || intermediate <= 0) return KVH_E_SHAPE;
+  if (intermediate % 8 != 0) return KVH_E_UNSUPPORTED;
+  if (num_tokens == 0) return KVH_OK;
+  if (!gate_up || !out) return KVH_E_NULL;
+  if (gate_up_tok_stride < 2 * (int64_t)intermediate || out_tok_stride < intermediate) return KVH_E_SHAPE;
+  if (gate_up_tok_stride % 8 || out_tok_stride % 8 || !a16(gate_up) || !a16(out)) return KVH_E_ALIGN;
+  return launch_silu_mul(gate_up, gate_up_tok_stride, out, out_tok_stride, num_tokens, intermediate, dtype,
+                         (hipStream_t)stream);
+}
+
+int kvh_gemv(const void* x, int64_t x_row_stride, const void* weight, int64_t w_row_stride, void* y,
+             int64_t y_row_stride, int32_t m, int32_t n, int32_t k, int32_t dtype, void* stream) {
+  if (dtype != KVH_DTYPE_F16 && dtype != KVH_DTYPE_BF16) return KVH_E_DTYPE;
+  if (m < 0 || n < 0 || k <= 0) return KVH_E_SHAPE;
+  if (m > 8 || k % 8 != 0) return KVH_E_UNSUPPORTED;
+  if (m == 0 || n == 0) return KVH_OK;
+  if (!x || !weight || !y) return KVH_E_NULL;
+  if (x_row_stride < k || w_row_stride < k || y_row_stride < n) return KVH_E_SHAPE;
+  if (x_row_stride % 8 || w_row_stride % 8 || !a16(x) || !a16(weight) || ((uintptr_t)y & 1u)) return KVH_E_ALIGN;
+  return launch_gemv(x, x_row_stride, weight, w_row_stride, y, y_row_stride, m, n, k, dtype, (hipStream_t)stream);
+}
+
 int kvh_profile_arm(void* const* events, int32_t num_events) {
   if (!events || num_events <= 0) {
     g_prof.num_events = 0;

@@ -110,6 +110,15 @@ struct MetaParams {
 
 int launch_prepare_metadata(const MetaParams& m, const int32_t* updates, int32_t num_updates, hipStream_t s);
 
+// Engine-harness kernels (engine_ops.hip).
+int launch_add_rmsnorm(const void* x, int64_t x_ts, const void* d, int64_t d_ts, const void* w, void* xo,
+                       int64_t xo_ts, void* h, int64_t h_ts, int64_t T, int32_t hd, float eps, int32_t dtype,
+                       hipStream_t s);
+int launch_silu_mul(const void* gu, int64_t gu_ts, void* out, int64_t o_ts, int64_t T, int32_t inter, int32_t dtype,
+                    hipStream_t s);
+int launch_gemv(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int32_t m, int32_t n,
+                int32_t k, int32_t dtype, hipStream_t s);
+
 int launch_rope_and_cache(const void* qkv, int64_t qkv_ts, const int64_t* positions, const float* cos_t,
                           const float* sin_t, int64_t max_pos, void* q_out, int64_t q_ts, int64_t q_hs, void* kc,
                           const int64_t* kcs, void* vc, const int64_t* vcs, const int64_t* slots, int64_t T,

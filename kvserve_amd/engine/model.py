@@ -4,7 +4,9 @@ The layer structure is the reference's (src/kvserve/model.py): tokens of all seq
 packed without padding, fused QKV and gate/up projections, K/V written to and read from
 the shared paged pool through `backend.write_kv` / `backend.forward`, and the forward pass
 split at the attention calls into num_layers + 1 row-wise pieces (model.py:187-212).
-GEMMs, norms and RoPE are PyTorch (hipBLASLt GEMMs on ROCm); attention is the backend's.
+GEMMs, norms and RoPE are PyTorch (hipBLASLt GEMMs on ROCm); attention is the backend's. On
+the GPU with 16-bit weights (`fused_ops`), the residual add + RMSNorm and SiLU * up run as
+single libkvhip kernels and projections of at most 8 rows as its GEMV (engine/ops.py).
 """
 
 from __future__ import annotations
@@ -17,6 +19,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from kvserve_amd.attention import AttentionMetadata, HipAttention
+from kvserve_amd.engine import ops
 from kvserve_amd.engine.config import ModelConfig
 
 
@@ -164,6 +167,8 @@ class LlamaForCausalLM(nn.Module):
         self.rope = RotaryEmbedding(cfg, max_positions)
         # a backend with a fused RoPE + cache-write kernel takes the raw QKV projection
         self.fused_rope = bool(getattr(backend, "fused_rope_cache", False))
+        # libkvhip's fused elementwise kernels and GEMV (set on the GPU, 16-bit weights)
+        self.fused_ops = False
 
     @torch.inference_mode()
     def forward(self, input_ids: torch.Tensor, positions: torch.Tensor, kv_caches: torch.Tensor,
@@ -184,6 +189,8 @@ class LlamaForCausalLM(nn.Module):
         Row-wise, never touches the KV cache (model.py:187-212). Returns (x, q, k, v), or
         (final hidden states, None, None, None) for the last piece. With a fused-RoPE backend
         the piece stops at the QKV projection: (x, qkv, None, None)."""
+        if self.fused_ops:
+            return self._piece_fused(i, input_ids, positions, x, attn)
         if i == 0:
             x = self.embed_tokens(input_ids)
         else:
@@ -199,8 +206,37 @@ class LlamaForCausalLM(nn.Module):
         q, k, v = layer.self_attn.project(h, positions, self.rope)
         return x, q, k, v
 
+    def _piece_fused(self, i: int, input_ids, positions, x, attn):
+        """piece() with libkvhip's kernels: the same operations, the residual adds fused into
+        the following norm, SiLU * up in one pass and small-batch projections on the GEMV."""
+        n = len(self.layers)
+        if i == 0:
+            x, h = ops.add_rmsnorm(self.embed_tokens(input_ids), None, self.layers[0].input_layernorm.weight,
+                                   self.layers[0].input_layernorm.eps)  # fmt: skip
+        else:
+            prev = self.layers[i - 1]
+            o = ops.linear(attn.flatten(1), prev.self_attn.o_proj.weight)
+            x, h = ops.add_rmsnorm(x, o, prev.post_attention_layernorm.weight, prev.post_attention_layernorm.eps)
+            d = ops.linear(ops.silu_mul(ops.linear(h, prev.mlp.gate_up_proj.weight)), prev.mlp.down_proj.weight)
+            norm = self.norm if i == n else self.layers[i].input_layernorm
+            x, h = ops.add_rmsnorm(x, d, norm.weight, norm.eps)
+            if i == n:
+                return h, None, None, None
+        layer = self.layers[i]
+        qkv = ops.linear(h, layer.self_attn.qkv_proj.weight)
+        if self.fused_rope:
+            return x, qkv, None, None
+        q, k, v = qkv.split([layer.self_attn.q_size, layer.self_attn.kv_size, layer.self_attn.kv_size], dim=-1)
+        q = q.view(-1, layer.self_attn.num_heads, layer.self_attn.head_dim)
+        k = k.view(-1, layer.self_attn.num_kv_heads, layer.self_attn.head_dim)
+        v = v.view(-1, layer.self_attn.num_kv_heads, layer.self_attn.head_dim)
+        q, k = self.rope(q, k, positions)
+        return x, q, k, v
+
     @torch.inference_mode()
     def compute_logits(self, hidden: torch.Tensor) -> torch.Tensor:
+        if self.fused_ops:
+            return ops.linear(hidden, self.lm_head.weight).float()
         return self.lm_head(hidden).float()
 
     # -- weights ----------------------------------------------------------------------------
@@ -254,8 +290,10 @@ class LlamaForCausalLM(nn.Module):
 
 
 def build_model(cfg: ModelConfig, device, dtype: torch.dtype, max_positions: int, backend=HipAttention,
-                weights: Path | None = None, seed: int = 0, std: float = 0.02) -> LlamaForCausalLM:  # fmt: skip
-    """Model on `device` in `dtype`: weights from a safetensors directory, else synthetic."""
+                weights: Path | None = None, seed: int = 0, std: float = 0.02,
+                fused_ops: bool | None = None) -> LlamaForCausalLM:  # fmt: skip
+    """Model on `device` in `dtype`: weights from a safetensors directory, else synthetic.
+    fused_ops (default: on a GPU with 16-bit weights) selects libkvhip's layer kernels."""
     with torch.device("meta"):
         model = LlamaForCausalLM(cfg, max_positions, backend)
     model = model.to(dtype).to_empty(device=device)  # never materialise fp32 weights
@@ -266,4 +304,8 @@ def build_model(cfg: ModelConfig, device, dtype: torch.dtype, max_positions: int
     else:
         model.init_random(seed, std)
     model.rope = RotaryEmbedding(cfg, max_positions, device=device)  # fp32 tables, after the cast
+    probe = torch.empty(0, dtype=dtype, device=device)
+    model.fused_ops = ops.enabled(probe) if fused_ops is None else bool(fused_ops)
+    if model.fused_ops and not ops.enabled(probe):
+        raise ValueError("fused_ops needs a GPU and fp16 / bf16 weights")
     return model.eval()

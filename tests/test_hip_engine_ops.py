@@ -1,0 +1,100 @@
+"""libkvhip's engine-harness kernels (kvh_add_rmsnorm, kvh_silu_mul, kvh_gemv) against the
+PyTorch operations they replace in the Llama layer (src/kvserve/model.py:22-32 and its MLP),
+in bf16 and fp16. The residual sum is bit-exact (one rounding, as PyTorch's add). The norm's
+fp32 statistics differ in summation order and rsqrt, and its output is rounded twice (x * r to
+the storage type, then times the weight), so it agrees to two units in the last place; SiLU
+(exp implementations differ) to one. The GEMV is checked against an fp32 product."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from kvserve_amd.engine import LLAMA_3_2_1B, ops
+from kvserve_amd.engine.model import build_model
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.bfloat16, torch.float16]
+
+
+def _ulp_close(got: torch.Tensor, want: torch.Tensor, ulps: int = 1) -> None:
+    assert got.dtype == want.dtype and got.shape == want.shape
+    g, w = got.float(), want.float()
+    eps = torch.finfo(want.dtype).eps
+    tol = ulps * eps * torch.maximum(g.abs(), w.abs()) + torch.finfo(want.dtype).tiny
+    bad = (g - w).abs() > tol
+    assert not bad.any(), f"{int(bad.sum())} elements beyond {ulps} ulp; worst {((g - w).abs() / tol).max():.2f}"
+
+
+def _rmsnorm(x, w, eps):  # model.py RMSNorm
+    x32 = x.float()
+    return w * (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("T,hd", [(1, 2048), (7, 4096), (300, 8192), (2, 136)])
+def test_add_rmsnorm(hip_device, dtype, T, hd):
+    g = torch.Generator(device=hip_device).manual_seed(T + hd)
+    x = torch.randn(T, hd, generator=g, device=hip_device).to(dtype)
+    d = (torch.randn(T, hd, generator=g, device=hip_device) * 3).to(dtype)
+    w = (torch.rand(hd, generator=g, device=hip_device) + 0.5).to(dtype)
+    xo, h = ops.add_rmsnorm(x, d, w, 1e-5)
+    assert torch.equal(xo, x + d)
+    _ulp_close(h, _rmsnorm(x + d, w, 1e-5), ulps=2)
+    x2, h2 = ops.add_rmsnorm(x, None, w, 1e-6)
+    assert x2 is x
+    _ulp_close(h2, _rmsnorm(x, w, 1e-6), ulps=2)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("T,inter", [(1, 8192), (5, 14336), (513, 64)])
+def test_silu_mul(hip_device, dtype, T, inter):
+    g = torch.Generator(device=hip_device).manual_seed(inter)
+    gu = (torch.randn(T, 2 * inter, generator=g, device=hip_device) * 4).to(dtype)
+    gate, up = gu.chunk(2, dim=-1)
+    _ulp_close(ops.silu_mul(gu), F.silu(gate) * up)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("m", [1, 2, 3, 8])
+@pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 14336), (1003, 1032), (28672, 2048), (5, 8)])
+def test_gemv_against_fp32(hip_device, dtype, m, n, k):
+    g = torch.Generator(device=hip_device).manual_seed(m * n + k)
+    x = torch.randn(m, k, generator=g, device=hip_device).to(dtype)
+    w = (torch.randn(n, k, generator=g, device=hip_device) * 0.05).to(dtype)
+    got = ops.gemv(x, w)
+    ref = x.float() @ w.float().t()
+    # fp32 accumulation in a different order, then one rounding to dtype
+    tol = 2 * torch.finfo(dtype).eps * ref.abs() + 1e-3 * ref.abs().max()
+    assert ((got.float() - ref).abs() <= tol).all()
+
+
+def test_gemv_strided_rows_and_large_batches_fall_back(hip_device):
+    x = torch.randn(3, 4096 + 64, device=hip_device).to(torch.bfloat16)[:, :4096]
+    w = torch.randn(512, 4096, device=hip_device).to(torch.bfloat16)
+    ref = x.float() @ w.float().t()
+    assert (ops.linear(x, w).float() - ref).abs().max() <= 0.05 * ref.abs().max()
+    big = torch.randn(ops.GEMV_MAX_ROWS + 1, 4096, device=hip_device).to(torch.bfloat16)
+    assert torch.equal(ops.linear(big, w), F.linear(big, w))
+
+
+def test_fused_model_matches_the_unfused_model(hip_device):
+    """The same bf16 weights through piece() with and without the fused kernels: logits of a
+    prefill and of decode-sized batches (the GEMV path) agree within bf16 accuracy."""
+    cfg = LLAMA_3_2_1B.with_layers(2)
+    models = [build_model(cfg, hip_device, torch.bfloat16, 512, seed=7, std=0.03, fused_ops=f) for f in (True, False)]
+    assert models[0].fused_ops and not models[1].fused_ops
+    for T in (1, 5, 64):
+        ids = torch.arange(T, device=hip_device) * 131 % cfg.vocab_size
+        outs = []
+        for mdl in models:
+            with torch.inference_mode():
+                x, qkv, _, _ = mdl.piece(0, ids, None, None, None)
+                attn = qkv[:, : cfg.num_heads * cfg.head_dim].reshape(T, cfg.num_heads, cfg.head_dim)
+                h, _, _, _ = mdl.piece(1, ids, None, x, attn)
+                x2, _, _, _ = mdl.piece(2, ids, None, h, attn)
+                outs.append(mdl.compute_logits(x2))
+        scale = outs[1].abs().max().item()
+        assert (outs[0] - outs[1]).abs().max().item() <= 0.03 * scale, T
