@@ -181,3 +181,84 @@ def test_every_code_reaches_the_output_exactly(hip_device, D):
     out = HipAttention.forward(q, kc, vc, meta, D**-0.5, k_scale=0.5, v_scale=4.0)
     want = fp8.dequantize(vals.view(FP8), 4.0)  # [B, Hkv, D]; G = 1
     assert torch.equal(out.float().cpu(), want)
+
+
+@pytest.mark.parametrize("D,BS", [(128, 32), (64, 64)])
+def test_other_block_sizes(hip_device, D, BS):
+    w = workloads.custom("fp8_bs", [1, 40, 1, 9], [100, 70, 3000, 0], 32, 8, D, BS, seed=6)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=6)
+    kc, vc = _fp8_caches(b, 0.75, 1.25)
+    out = _attend_fp8(b, kc, vc, 0.75, 1.25)
+    err = (out.float().cpu() - _oracle(b, kc, vc, 0.75, 1.25)).abs().max().item()
+    assert err <= pc.TOL_16BIT, err
+
+
+def test_decode_graph_replays_match_eager(hip_device):
+    """write_kv + forward over E4M3 caches captured once (the decode graph's static buffers,
+    cuda_graph.py:54-76) and replayed with new inputs: each replay equals an eager call bit
+    for bit and the dequantized oracle within the 16-bit bar."""
+    import random
+
+    dev = hip_device
+    H, Hkv, D, BS, NB, bucket, width_max = 32, 8, 128, 16, 900, 8, 128
+    k_scale, v_scale = 0.5, 0.75
+    gen = torch.Generator(device=dev).manual_seed(9)
+    kc = fp8.quantize(torch.randn(NB + 1, BS, Hkv, D, generator=gen, device=dev), k_scale).to(dev)
+    vc = fp8.quantize(torch.randn(NB + 1, BS, Hkv, D, generator=gen, device=dev), v_scale).to(dev)
+    q = torch.zeros(bucket, H, D, device=dev, dtype=torch.bfloat16)
+    k = torch.zeros(bucket, Hkv, D, device=dev, dtype=torch.bfloat16)
+    v = torch.zeros(bucket, Hkv, D, device=dev, dtype=torch.bfloat16)
+    meta = AttentionMetadata(
+        slot_mapping=torch.full((bucket,), NB * BS, dtype=torch.long, device=dev),
+        block_tables=torch.full((bucket, width_max), NB, dtype=torch.long, device=dev),
+        seq_lens=torch.ones(bucket, dtype=torch.long, device=dev),
+        query_lens=torch.ones(bucket, dtype=torch.long, device=dev),
+        query_start_loc=torch.arange(bucket + 1, dtype=torch.long, device=dev),
+        max_seq_len=1,
+        max_query_len=1,
+    )
+
+    def step():
+        HipAttention.write_kv(kc, vc, k, v, meta.slot_mapping, k_scale=k_scale, v_scale=v_scale)
+        return HipAttention.forward(q, kc, vc, meta, D**-0.5, k_scale=k_scale, v_scale=v_scale)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step()
+    rng = random.Random(2)
+    ids = list(range(NB))
+    for it in range(4):
+        n = rng.choice([2, 5, 8])
+        lens = [rng.randint(1, 2000) for _ in range(n)]
+        rng.shuffle(ids)
+        tables, i = [], 0
+        for L in lens:
+            tables.append(ids[i : i + -(-L // BS)])
+            i += len(tables[-1])
+        width = max(len(t) for t in tables)
+        rows = [t + [NB] * (width - len(t)) for t in tables] + [[NB] * width] * (bucket - n)
+        slots = [t[(L - 1) // BS] * BS + (L - 1) % BS for t, L in zip(tables, lens)]
+        q.copy_(torch.randn(bucket, H, D, generator=gen, device=dev).to(torch.bfloat16))
+        k.copy_(torch.randn(bucket, Hkv, D, generator=gen, device=dev).to(torch.bfloat16))
+        v.copy_(torch.randn(bucket, Hkv, D, generator=gen, device=dev).to(torch.bfloat16))
+        meta.slot_mapping.copy_(torch.tensor(slots + [NB * BS] * (bucket - n)))
+        meta.seq_lens.copy_(torch.tensor(lens + [1] * (bucket - n)))
+        meta.block_tables[:, :width].copy_(torch.tensor(rows))
+        graph.replay()
+        replayed = out.clone()
+        torch.cuda.synchronize()
+        eager = HipAttention.forward(q, kc, vc, meta, D**-0.5, k_scale=k_scale, v_scale=v_scale)
+        torch.cuda.synchronize()
+        assert torch.equal(replayed.view(torch.int16), eager.view(torch.int16)), it
+        ref = torch_reference.forward(
+            q[:n].float().cpu(), fp8.dequantize(kc.cpu(), k_scale), fp8.dequantize(vc.cpu(), v_scale),
+            meta.block_tables[:n].cpu(), meta.seq_lens[:n].cpu(), torch.ones(n, dtype=torch.long), D**-0.5,
+        )  # fmt: skip
+        assert (replayed[:n].float().cpu() - ref).abs().max().item() <= pc.TOL_16BIT, it
