@@ -926,7 +926,9 @@ struct PfLoads {
   uint32_t loff[L::kLoadsPerWave];
 };
 
-template <int D>
+// EB: bytes per cache element (2; 1 for an E4M3 cache, whose granules are the same 8
+// elements in 8 bytes, converted on their way to the 16-bit stage).
+template <int D, int EB = 2>
 __device__ __forceinline__ void pf_loads_init(PfLoads<D>& pl, const PAParams& p, int w, int kvh) {
   using L = PrefillLds<D>;
   const int lane = threadIdx.x & 63;
@@ -934,16 +936,16 @@ __device__ __forceinline__ void pf_loads_init(PfLoads<D>& pl, const PAParams& p,
   const int g0 = w * L::kLoadsPerWave;
   const bool v = g0 / L::kLoadsPerTile != 0;
   const int i0 = g0 % L::kLoadsPerTile;
-  pl.sb2 = 2 * (v ? p.v_sb : p.k_sb);
-  pl.ss2 = 2 * (v ? p.v_ss : p.k_ss);
-  pl.cache = (const char*)(v ? p.vc : p.kc) + (int64_t)kvh * (v ? p.v_sh : p.k_sh) * 2;
+  pl.sb2 = EB * (v ? p.v_sb : p.k_sb);
+  pl.ss2 = EB * (v ? p.v_ss : p.k_ss);
+  pl.cache = (const char*)(v ? p.vc : p.kc) + (int64_t)kvh * (v ? p.v_sh : p.k_sh) * EB;
   pl.h = i0 * L::kRowsPerLoad / 16;
   pl.dst = (v ? L::kTileBytes : 0) + i0 * 1024;
   if (!v) {
 #pragma unroll
     for (int k = 0; k < L::kLoadsPerWave; ++k) {
       const int row = (i0 + k) * L::kRowsPerLoad + row_in;  // row of the chunk (0..31)
-      pl.loff[k] = (uint32_t)((row % 16) * pl.ss2) + 16u * (uint32_t)(slot ^ (row % L::kSlots));
+      pl.loff[k] = (uint32_t)((row % 16) * pl.ss2) + 8u * EB * (uint32_t)(slot ^ (row % L::kSlots));
     }
   } else {
     // V stage layout: blocks b = h (D/16) + i of 512 bytes, block b holding d = 16i .. 16i+15
@@ -954,7 +956,7 @@ __device__ __forceinline__ void pf_loads_init(PfLoads<D>& pl, const PAParams& p,
     for (int k = 0; k < L::kLoadsPerWave; ++k) {
       const int P = 64 * (i0 + k) + lane;
       const int b = P / 32, tok = (P % 32) / 2, chunk = 2 * (b % (D / 16)) + P % 2;
-      pl.loff[k] = (uint32_t)(tok * pl.ss2) + 16u * (uint32_t)chunk;
+      pl.loff[k] = (uint32_t)(tok * pl.ss2) + 8u * EB * (uint32_t)chunk;
     }
   }
 }
@@ -1347,6 +1349,164 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
   pf_write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, slot * kPrefillRows - wg_row0);
 }
 
+// prefill_tile over an E4M3 cache. Direct global->LDS loads cannot convert, so each lane
+// loads, as E4M3, the 8-element granules the DMA would have moved (half the bytes, the
+// same offsets halved), converts them exactly to E's 16-bit type and writes them to the LDS
+// positions the DMA would have filled: the stage layout, the operand reads and the compute
+// are those of prefill_tile. Two register sets keep the loads two chunks ahead; chunk i is
+// converted and written right before the barrier that publishes it, so two LDS stages
+// suffice (stage i % 2 was last read by chunk i - 2, before the previous barrier).
+template <class E, int D>
+__device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, const SeqView& sv, int R, int seq,
+                                                 int kvh, int t, int c_lo, int c_hi, int w, bool partial,
+                                                 int64_t slot, int rest, int total) {
+  constexpr int NT = kPrefillNQT;
+  using L = PrefillLds<D>;
+  constexpr int KLW = L::kLoadsPerWave;
+  typedef __attribute__((address_space(3))) u32x4* lds_u32x4_ptr;
+  c_lo = uni(c_lo);
+  c_hi = uni(c_hi);
+  const int lane = threadIdx.x & 63;
+  const int wg_row0 = t * kPrefillRows;
+  const int wg_last = min(wg_row0 + kPrefillRows - 1, R - 1);
+  const int kv_lim = (int)clamp64(sv.ctx + wg_last / p.G + 1, 0, sv.kv_total);
+  const int row0 = wg_row0 + w * 16 * NT;
+  const int my_last = min(row0 + 16 * NT - 1, R - 1);
+  const int my_lim = row0 < R ? (int)clamp64(sv.ctx + my_last / p.G + 1, 0, sv.kv_total) : 0;
+  const int lim_all = row0 < R ? (int)clamp64(sv.ctx + row0 / p.G + 1, 0, sv.kv_total) : 0;
+
+  WaveState<D, NT> s;
+  load_q<D, NT>(s, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
+  float c = fabsf(p.qk_scale);
+  if (p.qk_scale < 0.f) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int cc = 0; cc < D / 32; ++cc) s.q[t][cc] ^= 0x80008000u;
+  } else if (p.qk_scale == 0.f) {
+    c = 1.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int cc = 0; cc < D / 32; ++cc) s.q[t][cc] = u32x4{0u, 0u, 0u, 0u};
+  }
+  const int64_t* btrow = p.bt + (int64_t)seq * p.bt_rs;
+  const int page_end = (kv_lim + p.BS - 1) / p.BS;
+  PfLoads<D> pl;
+  pf_loads_init<D, 1>(pl, p, w, kvh);
+  uint32_t ka[D / 32];
+  pf_k_lanes<D>(ka, lds);
+  const uint32_t vbase = lds_lane_addr(lds, 8);
+  PfWindow win;
+  pf_window(win, p, btrow, c_lo, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
+
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();  // every wave has finished reading the stages (previous tile)
+  __builtin_amdgcn_sched_barrier(0);
+  const int n = c_hi - c_lo;
+  const int n_my = max(0, min(n, (my_lim + kChunk - 1) / kChunk - c_lo));
+  int n_int = max(0, min(n_my, min(lim_all / kChunk, win.first_bad) - c_lo));
+
+  u32x2 raw[2][KLW];
+  auto issue = [&](u32x2 (&r)[KLW], int ci) {
+    const int rel = ci - win.c0;
+    const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(win.off_hi, rel) << 32) |
+                       (uint32_t)__builtin_amdgcn_readlane(win.off_lo, rel);
+    uint64_t base = (uint64_t)(uintptr_t)pl.cache + o;
+    asm volatile("" : "+s"(base));
+#pragma unroll
+    for (int k = 0; k < KLW; ++k) {
+      uint32_t off = pl.loff[k];
+      asm volatile("" : "+v"(off));
+      r[k] = *(const u32x2*)((const char*)(uintptr_t)base + off);
+    }
+  };
+  issue(raw[0], c_lo);
+  if (n > 1) issue(raw[1], c_lo + 1);
+
+  // step i: wait for chunk i's bytes, convert them into stage i % 2, publish, load chunk i + 2
+  auto sync = [&](int i, auto set) {
+    constexpr int S = decltype(set)::value;
+    const int left = rest + (n - i);  // wave priority as in prefill_tile
+    const int lvl = min(3, (4 * left) / (total + 1));
+    if (lvl >= 2)
+      lvl == 3 ? __builtin_amdgcn_s_setprio(3) : __builtin_amdgcn_s_setprio(2);
+    else
+      lvl == 1 ? __builtin_amdgcn_s_setprio(1) : __builtin_amdgcn_s_setprio(0);
+    const int ci2 = c_lo + i + 2;
+    if (i + 2 < n && ci2 - win.c0 >= 64) {
+      pf_window(win, p, btrow, c_lo + i, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
+      n_int = min(n_int, win.first_bad - c_lo);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + 1 < n)
+      wait_vm<KLW>();  // chunk i + 1 may stay in flight
+    else
+      wait_vm<0>();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < KLW; ++k) {
+      const u32x2 r = raw[S][k];
+      const u32x4 o = {E::template from_fp8x2<false>(r[0]), E::template from_fp8x2<true>(r[0]),
+                       E::template from_fp8x2<false>(r[1]), E::template from_fp8x2<true>(r[1])};
+      *(lds_u32x4_ptr)(uintptr_t)((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds +
+                                  (uint32_t)(S * L::kStageBytes + pl.dst + k * 1024 + 16 * lane)) = o;
+    }
+    __syncthreads();  // the stage's writes are complete and visible; nothing else in flight
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + 2 < n) issue(raw[S], ci2);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // chunk i from the stage at byte offset SOFF + stage (one masked instance with a runtime
+  // stage: two static ones in the masked loop double the live ranges and spill)
+  auto compute = [&](int i, int stage, auto soff, auto masked) {
+    constexpr int SOFF = decltype(soff)::value;
+    constexpr bool MASKED = decltype(masked)::value;
+    f32x4 sc[NT][2];
+    pf_scores_lds<E, D, NT>(s, ka, SOFF + stage, sc);
+    ChunkRef cr;
+    cr.tok0 = (c_lo + i) * kChunk;
+    cr.blk[0] = cr.blk[1] = 0;
+    if (MASKED) {
+      const int rel = c_lo + i - win.c0;
+      cr.blk[0] = (win.ok0 >> rel) & 1 ? 0 : -1;
+      cr.blk[1] = (win.ok1 >> rel) & 1 ? 0 : -1;
+      pf_mask<NT>(sc, s.limit, cr);
+    }
+    float mx[NT];
+    pf_lanemax<NT>(sc, mx);
+    __builtin_amdgcn_sched_barrier(0);
+    VTr<D> vt;
+    const uint32_t vb = vbase + (uint32_t)stage;
+    pf_v_issue<D, SOFF + L::kTileBytes, 0, kVLead>(vt, vb);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 pt[NT];
+    pf_softmax<E, D, NT>(s, sc, mx, c, pt);
+    pf_pv<E, D, NT, MASKED, SOFF + L::kTileBytes>(s, vt, vb, cr, sv.kv_total, pt);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, L::kStageBytes>;
+  int i = 0;
+  while (i < n_int) {  // unmasked, unrolled by the two stages
+    sync(i, I0{});
+    compute(i, 0, S0{}, std::false_type{});
+    if (++i >= n_int) break;
+    sync(i, I1{});
+    compute(i, 0, S1{}, std::false_type{});
+    ++i;
+  }
+  for (; i < n; ++i) {  // masked, then past this wave's rows (loads, conversions, barriers)
+    if (i & 1)
+      sync(i, I1{});
+    else
+      sync(i, I0{});
+    if (i < n_my) compute(i, (i & 1) * L::kStageBytes, S0{}, std::true_type{});
+  }
+  pf_write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, slot * kPrefillRows - wg_row0);
+}
+
 // Chunks of tile t (rows 128 t .. of R): those its last row can see, at least one so that
 // every tile is visited and written.
 __device__ __forceinline__ int pre_tile_chunks(const PAParams& p, const SeqView& sv, int R, int t) {
@@ -1465,10 +1625,10 @@ __device__ void plan_prefill(const PAParams& p) {
 // dealt to the 8 XCDs round-robin, so the units are numbered XCD by XCD: the units of one
 // XCD are contiguous in the flat space and read the same sequence's K/V through that
 // XCD's L2.
-template <class E, int D>
-__global__ __launch_bounds__(256, 3) void pa_prefill_kernel(PAParams p) {
+template <class E, int D, bool KV8>
+__global__ __launch_bounds__(256, KV8 ? 2 : 3) void pa_prefill_kernel(PAParams p) {
   using L = PrefillLds<D>;
-  __shared__ __attribute__((aligned(1024))) char lds[L::kStages * L::kStageBytes];
+  __shared__ __attribute__((aligned(1024))) char lds[(KV8 ? 2 : L::kStages) * L::kStageBytes];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int32_t* job = p.ws_job + (int64_t)(kMaxDecodeWaves + blockIdx.x) * kJobInts;
   if (threadIdx.x == 0) job[0] = kJobNone;
@@ -1507,8 +1667,11 @@ __global__ __launch_bounds__(256, 3) void pa_prefill_kernel(PAParams p) {
     if (c_hi > c_lo) {
       const bool whole = c_lo == 0 && c_hi == n_t;
       const int64_t slot = 2 * (int64_t)u + (first ? 0 : 1);
-      prefill_tile<E, D>(lds, p, sv, R, seq, kvh, t, c_lo, c_hi, w, !whole, slot, (int)(x1 - (x + (b - a))),
-                         (int)(x1 - (u * C / NUa)));
+      const int rest = (int)(x1 - (x + (b - a))), total = (int)(x1 - (u * C / NUa));
+      if constexpr (KV8)
+        prefill_tile_kv8<E, D>(lds, p, sv, R, seq, kvh, t, c_lo, c_hi, w, !whole, slot, rest, total);
+      else
+        prefill_tile<E, D>(lds, p, sv, R, seq, kvh, t, c_lo, c_hi, w, !whole, slot, rest, total);
       if (threadIdx.x == 0 && c_lo == 0 && c_hi < n_t) {
         // the tile continues in units u + 1 .. u1, each holding it as its first piece
         const int64_t x_last = x + (tw - a) - 1;
@@ -1533,39 +1696,6 @@ __global__ __launch_bounds__(256, 3) void pa_prefill_kernel(PAParams p) {
     }
     n_t = pre_tile_chunks(p, sv, R, t);
   }
-}
-
-// ---------------------------------------------------------------------------------------
-// Prefill class over an E4M3 cache. The LDS ring of pa_prefill_kernel is filled by direct
-// global->LDS loads, which cannot convert; this kernel instead reuses the decode path's
-// register pipeline (load, convert exactly to 16-bit operands, MFMA) with 16 kRowTileNT
-// query rows per wave and each wave walking the whole context its rows see. Workgroup
-// (x, kvh, k): its 4 waves take row tiles 4x .. 4x + 3 of kv head kvh of the k-th
-// prefill-class sequence (list and count from the prefill plan); a tile past the sequence's
-// rows, or a k past the count, exits at once. The 4 waves read the same K/V (through L2).
-// Measured at C3: 16 rows per wave 115 us, 32 rows 120 us, 64 rows 167 us (more waves
-// resident beat fewer K/V re-reads).
-constexpr int kRowTileNT = 1;  // 16-row tiles per wave of pa_rowtile_kernel (1: most waves, measured best)
-
-template <class E, int D>
-__global__ __launch_bounds__(256) void pa_rowtile_kernel(PAParams p) {
-  constexpr int NT = kRowTileNT, RW = 16 * NT;  // rows per wave
-  const int n_pre = (int)uni64(p.ws_plan_hdr[2]);
-  const int k = blockIdx.z;
-  if (k >= n_pre) return;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kvh = blockIdx.y;
-  const int seq = uni(p.ws_pre_list[k]);
-  const SeqView sv = seq_view_uniform(p, seq);
-  const int R = sv.q_len * p.G;
-  const int row0 = (blockIdx.x * kWavesPerWG + wave) * RW;
-  if (row0 >= R) return;
-  const int last = min(R, row0 + RW) - 1;
-  const int tok_hi = (int)clamp64(sv.ctx + last / p.G + 1, 0, sv.kv_total);
-  WaveState<D, NT> st;
-  load_q<D, NT, true>(st, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
-  run_chunks<E, D, NT, true>(st, p, p.bt + (int64_t)seq * p.bt_rs, kvh, 0, kChunk, tok_hi, sv.kv_total);
-  write_rows<E, D, NT>(st, p, sv, R, row0, kvh, false, nullptr, nullptr, 0);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1608,9 +1738,9 @@ template <class E, int D, bool KV8>
 static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipStream_t s, LaunchLog& log) {
   int err = 0;
   p.PLAN = plan.launch_prefill ? 1 : 0;
-  if (plan.launch_prefill && !KV8) {
+  if (plan.launch_prefill) {
     // the unit count is fixed before the decode launch: both kernels write merge jobs
-    int units = resident_blocks((const void*)&pa_prefill_kernel<E, D>);
+    int units = resident_blocks((const void*)&pa_prefill_kernel<E, D, KV8>);
     if (units > kMaxPrefillUnits) units = kMaxPrefillUnits;
     p.NUP = units / 8 * 8;
     if (p.NUP < 8) p.NUP = 8;
@@ -1625,16 +1755,7 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipSt
   if (err) return err;
   log.after_launch(1, s);
   if (plan.launch_prefill) {
-    if constexpr (KV8) {
-      // prefill-class sequences have q_len > QS, so at most T / (QS + 1) of them
-      const int tiles = (int)(((int64_t)max_q * p.G + 16 * kRowTileNT - 1) / (16 * kRowTileNT));
-      const int64_t most = p.T / (p.QS + 1);
-      const int seqs = (int)(most < p.B ? (most > 0 ? most : 1) : p.B);
-      const dim3 grid((unsigned)((tiles + kWavesPerWG - 1) / kWavesPerWG), (unsigned)p.Hkv, (unsigned)seqs);
-      hipLaunchKernelGGL((pa_rowtile_kernel<E, D>), grid, dim3(256), 0, s, p);
-    } else {
-      hipLaunchKernelGGL((pa_prefill_kernel<E, D>), dim3(p.NUP), dim3(256), 0, s, p);
-    }
+    hipLaunchKernelGGL((pa_prefill_kernel<E, D, KV8>), dim3(p.NUP), dim3(256), 0, s, p);
     if ((err = (int)hipGetLastError())) return err;
     log.after_launch(2, s);
   }

@@ -4,7 +4,7 @@ oracle (oracle/fp8.py):
     (x.float() / scale).clamp(-448, 448).to(float8_e4m3fn) bit for bit;
   * attention over E4M3 caches matches the torch restatement of TorchAttention.forward run on
     the dequantized caches (e4m3 * scale, fp32) within the 16-bit bar (max-abs 2e-2), over the
-    reference's parity cases, D = 128 mixed batches (the prefill-class row-tile kernel) and
+    reference's parity cases, D = 128 mixed batches (the prefill kernel's E4M3 stages) and
     split decode segments;
   * every E4M3 byte reaches the output exactly (one-key sequences return V exactly).
 """
@@ -133,7 +133,7 @@ def test_reference_cases_fp8(hip_device, case, heads, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
-def test_d128_mixed_batch_uses_row_tiles(hip_device, dtype):
+def test_d128_mixed_batch_uses_the_prefill_kernel(hip_device, dtype):
     """Prefill-class sequences (q_len > 4 at G = 4) with cached context next to decode rows."""
     w = workloads.custom("fp8_mixed", [200, 1, 70, 1, 1, 33], [300, 900, 0, 2000, 17, 4000], 32, 8, 128, 16, seed=4)
     b = workloads.materialize(w, dtype, hip_device, seed=4)
