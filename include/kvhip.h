@@ -270,6 +270,7 @@ enum kvh_kernel_kind {
   KVH_KERNEL_PREFILL = 2,  /* stream-K prefill-class tiles (q_len large) */
   KVH_KERNEL_REDUCE = 3,   /* log-sum-exp merge of split decode segments and prefill tiles */
   KVH_KERNEL_F32 = 4,      /* exact fp32 path */
+  KVH_KERNEL_SHARE = 5,    /* shared-prefix plan of the cascade decode (long tables, decode-only batches) */
 };
 KVH_API int kvh_last_launch_kernels(int32_t* kinds, int32_t cap);
 

@@ -37,8 +37,6 @@ void LaunchLog::after_launch(int kind, hipStream_t s) {
 
 Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t W, int32_t BS, int32_t max_q,
                int32_t dtype) {
-  (void)W;
-  (void)BS;
   Plan pl{};
   pl.G = H / Hkv;
   if (max_q < 1) max_q = 1;
@@ -73,8 +71,18 @@ Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t 
                                                align_up(((size_t)B + 1) * sizeof(int64_t)) +
                                                align_up((size_t)kMaxPrefillUnits * 4 * sizeof(int32_t))
                                          : 0;
+    // cascade over a shared prefix: share header, decode list, prefix partials, merge jobs
+    pl.cascade = !pl.launch_prefill && pl.NT == 1 && B >= 2 && (int64_t)W * BS > kCascadeMinTokens;
+    pl.SG = pl.RS >= 16 ? 1 : 16 / pl.RS;
+    const int64_t nhg = Hkv / pl.HGW;
+    pl.xslots = pl.cascade ? ((int64_t)B + pl.SG - 1) / pl.SG * nhg + kMaxDecodeWaves / pl.HGW : 0;
+    pl.ws_x_bytes = pl.cascade ? align_up(kShareHdr * sizeof(int64_t)) + align_up((size_t)B * sizeof(int32_t)) +
+                                     align_up((size_t)pl.xslots * pl.HGW * 16 * D * sizeof(float)) +
+                                     align_up((size_t)pl.xslots * pl.HGW * 16 * 2 * sizeof(float)) +
+                                     align_up((size_t)B * nhg * kJobInts * sizeof(int32_t))
+                               : 0;
     pl.ws_bytes = pl.ws_acc_bytes + pl.ws_ml_bytes + pl.ws_job_bytes + pl.ws_pacc_bytes + pl.ws_pml_bytes +
-                  pl.ws_plan_bytes;
+                  pl.ws_plan_bytes + pl.ws_x_bytes;
   }
   (void)T;
   return pl;
@@ -390,6 +398,8 @@ static int paged_attention_impl(const void* q, int64_t q_tok_stride, int64_t q_h
   p.HGW = plan.HGW;
   p.NU = 0;   // set by the decode launcher from the device's occupancy
   p.NUP = 0;  // set by the prefill launcher likewise
+  p.CASC = 0;  // set by the launcher when the plan has the cascade path
+  p.SG = plan.SG;
   if (plan.ws_bytes) {
     char* w = (char*)workspace;
     p.ws_acc = (float*)w;
@@ -410,6 +420,19 @@ static int paged_attention_impl(const void* q, int64_t q_tok_stride, int64_t q_h
       p.ws_pre_beg = (int64_t*)w;
       w += align_up(((size_t)num_seqs + 1) * sizeof(int64_t));
       p.ws_pre_unit = (int32_t*)w;
+      w += align_up((size_t)kMaxPrefillUnits * 4 * sizeof(int32_t));
+    }
+    if (plan.ws_x_bytes) {
+      const size_t rows = (size_t)plan.xslots * plan.HGW * 16;
+      p.ws_share = (int64_t*)w;
+      w += align_up(kShareHdr * sizeof(int64_t));
+      p.ws_dec_list = (int32_t*)w;
+      w += align_up((size_t)num_seqs * sizeof(int32_t));
+      p.ws_xacc = (float*)w;
+      w += align_up(rows * head_dim * sizeof(float));
+      p.ws_xml = (float*)w;
+      w += align_up(rows * 2 * sizeof(float));
+      p.ws_xjob = (int32_t*)w;
     }
   }
 

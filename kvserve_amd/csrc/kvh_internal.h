@@ -14,6 +14,13 @@ constexpr int32_t kMaxDecodeWaves = 8192;
 constexpr int32_t kMaxPrefillUnits = 768;
 // Query rows ((token, head) pairs of one kv head) one prefill workgroup owns.
 constexpr int32_t kPrefillRows = 128;
+// Cascade decode over a shared prefix: planned when a decode-only batch has at most 16 query
+// rows per sequence (one 16-row tile) and block tables longer than kCascadeMinTokens; used
+// when the cascade members (decode-class sequences with at least kCascadeMinChunks chunks of
+// context) share at least kCascadeMinChunks chunks of table prefix.
+constexpr int32_t kCascadeMinTokens = 8192;
+constexpr int32_t kCascadeMinChunks = 8;
+constexpr int32_t kShareHdr = 8;  // int64: shared tokens, prefix groups, row of the shared table, sequences
 // Merge job record: int32 fields, one record per work unit (decode units first).
 constexpr int32_t kJobInts = 16;
 constexpr int32_t kMaxJobs = kMaxDecodeWaves + kMaxPrefillUnits;
@@ -44,6 +51,8 @@ struct PAParams {
   int32_t NU;      // work units the decode launch provides (waves / HGW)
   int32_t NUP;     // work units (workgroups) of the prefill launch (16-bit cache), else 0
   int32_t PLAN;    // 1: workgroup 0 of the decode launch writes the prefill plan
+  int32_t CASC;    // 1: the share kernel ran before the decode launch (cascade over a shared prefix)
+  int32_t SG;      // cascade: decode-class sequences per 16-row prefix group (16 / RS)
   float v_scale;   // factor of every output row: the V scale of an E4M3 cache, else 1
   float* ws_acc;   // [slots, HGW, RS, D] unnormalised partial outputs of split decode segments
   float* ws_ml;    // [slots, HGW, RS, 2] running max (exp2 domain) and sum of each partial
@@ -55,6 +64,12 @@ struct PAParams {
   int32_t* ws_pre_list;  // [B] the prefill-class sequences in order
   int64_t* ws_pre_beg;   // [B + 1] flat start of each (ws_pre_beg[n_pre] = C)
   int32_t* ws_pre_unit;  // [kMaxPrefillUnits, 4] start of unit u: list index, kv head, tile, offset
+  // cascade, written by pa_share_kernel before the decode launch:
+  int64_t* ws_share;     // [kShareHdr]: shared prefix tokens (multiple of 32, 0: none), groups, r0, sequences
+  int32_t* ws_dec_list;  // [B] decode-class sequences in order
+  float* ws_xacc;        // [xslots, HGW, 16, D] partials of the prefix segments
+  float* ws_xml;         // [xslots, HGW, 16, 2]
+  int32_t* ws_xjob;      // [B * Hkv / HGW, kJobInts] merge jobs per (sequence, head group)
 };
 
 // Launch plan: a pure function of static shapes (graph-capture safe).
@@ -62,8 +77,11 @@ struct Plan {
   int32_t G, QS, NT, RS;    // GQA group, decode-class q_len cap, 16-row tiles, rows per sequence
   int32_t HGW;              // kv heads per decode work unit
   bool launch_prefill;      // max_query_len > QS
+  bool cascade;             // the share kernel runs and the decode kernel may take the cascade path
+  int32_t SG;               // cascade: sequences per prefix group
+  int64_t xslots;           // cascade: prefix partial slots
   int64_t slots;            // partial slots: B * Hkv / HGW + kMaxDecodeWaves / HGW
-  size_t ws_acc_bytes, ws_ml_bytes, ws_job_bytes, ws_pacc_bytes, ws_pml_bytes, ws_plan_bytes, ws_bytes;
+  size_t ws_acc_bytes, ws_ml_bytes, ws_job_bytes, ws_pacc_bytes, ws_pml_bytes, ws_plan_bytes, ws_x_bytes, ws_bytes;
 };
 
 Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t W, int32_t BS, int32_t max_q,

@@ -667,10 +667,18 @@ __device__ __forceinline__ void write_job(int32_t* job, int kind, int pieces, in
 // (segment index + unit); the unit holding a split segment's first piece records a merge job.
 constexpr int kMinUnitChunks = 4;
 
-__device__ __forceinline__ int seq_chunks(const PAParams& p, int s) {
-  const SeqView v = seq_view(p, s);
+// A cascade member: a decode-class sequence with at least kCascadeMinChunks chunks of context
+// (so padding rows and short sequences never limit the shared length).
+__device__ __forceinline__ bool cascade_member(const PAParams& p, const SeqView& v) {
+  return v.q_len > 0 && v.q_len <= p.QS && clamp64(v.ctx, 0, v.kv_total) >= kCascadeMinChunks * kChunk;
+}
+
+// skip: keys [0, skip) of every cascade member are computed by the prefix segments
+// (skip <= its context then), so its own segments cover [skip, kv_total).
+__device__ __forceinline__ int seq_chunks(const PAParams& p, const SeqView& v, int skip) {
   if (v.q_len == 0 || v.q_len > p.QS) return 0;
-  return max(1, (v.kv_total + kChunk - 1) / kChunk);
+  const int sk = skip > 0 && cascade_member(p, v) ? skip : 0;
+  return max(1, (v.kv_total - sk + kChunk - 1) / kChunk);
 }
 
 // 64 sequences of the chunk prefix sum; lane l describes sequence blk0 + l.
@@ -680,23 +688,40 @@ struct SeqWindow {
   int c;      // this lane's sequence
   int excl;   // sequences blk0 .. blk0 + l - 1
   int total;  // the whole window
+  int nbase;  // cascade members before blk0
+  int nexcl;  // cascade members blk0 .. blk0 + l - 1
+  int ntotal; // cascade members of the whole window
+  int mem;    // this lane's sequence is a cascade member
 };
 
-__device__ __forceinline__ void scan_window(SeqWindow& sw, const PAParams& p, int blk0, int base) {
+__device__ __forceinline__ void scan_window(SeqWindow& sw, const PAParams& p, int blk0, int base, int nbase,
+                                            int skip) {
   const int lane = threadIdx.x & 63;
   const int s = blk0 + lane;
-  const int c = s < p.B ? seq_chunks(p, s) : 0;
-  int incl = c;
+  int c = 0, mem = 0;
+  if (s < p.B) {
+    const SeqView v = seq_view(p, s);
+    c = seq_chunks(p, v, skip);
+    mem = cascade_member(p, v) ? 1 : 0;
+  }
+  int incl = c, ninc = mem;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o);
-    if (lane >= o) incl += y;
+    const int y = __shfl_up(incl, o), z = __shfl_up(ninc, o);
+    if (lane >= o) {
+      incl += y;
+      ninc += z;
+    }
   }
   sw.blk0 = blk0;
   sw.base = base;
   sw.c = c;
   sw.excl = incl - c;
   sw.total = __builtin_amdgcn_readlane(incl, 63);  // uniform (a shuffle result would not be)
+  sw.nbase = nbase;
+  sw.nexcl = ninc - mem;
+  sw.ntotal = __builtin_amdgcn_readlane(ninc, 63);
+  sw.mem = mem;
 }
 
 __device__ __forceinline__ int64_t active_units(int64_t C, int NU) {
@@ -707,6 +732,186 @@ __device__ __forceinline__ int64_t active_units(int64_t C, int NU) {
 constexpr int kPlanThreads = 256;    // the decode kernel's workgroup
 constexpr int kPlanLdsSeqs = 1024;  // flat starts kept in LDS for the unit search (else global)
 __device__ void plan_prefill(const PAParams& p);
+
+// ---------------------------------------------------------------------------------------
+// Cascade decode over a shared prefix (prefix caching hands several sequences the same
+// physical blocks at the start of their tables). pa_share_kernel (one workgroup, before the
+// decode launch) lists the cascade members (decode-class sequences with kCascadeMinChunks
+// chunks of context or more) and finds the longest common table prefix: the first S blocks
+// of every member's table equal those of the first one (valid ids), and all their query rows
+// see those keys (S BS <= every member's context). The shared length L = min(S BS, smallest
+// member context) rounded down to 32-token chunks (0 when below kCascadeMinChunks chunks or
+// fewer than 2 members). The decode kernel then computes keys [0, L) once per group of SG
+// members (their query rows stacked into one 16-row tile, so the shared K/V are read
+// members / SG times instead of once per member) and each member's own keys [L, kv_total)
+// as usual; other sequences take their whole range as usual. The merge kernel combines the
+// partials of every (sequence, head group) from one record each.
+__device__ __forceinline__ int block_min(int v, int* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int r = red[0];
+#pragma unroll
+  for (int i = 1; i < kPlanThreads / 64; ++i) r = min(r, red[i]);
+  return r;
+}
+
+constexpr int kShareLdsList = 1024;  // members whose ids stay in LDS for the column compare
+constexpr int kShareCols = 4;        // columns per thread and pass
+constexpr int kShareRows = 8;        // member rows loaded together
+
+__global__ __launch_bounds__(kPlanThreads) void pa_share_kernel(PAParams p) {
+  __shared__ int s_wsum[kPlanThreads / 64];
+  __shared__ int red[kPlanThreads / 64];
+  __shared__ int s_list[kShareLdsList];
+  const int tid = threadIdx.x;
+  const int per = (p.B + kPlanThreads - 1) / kPlanThreads;
+  const int s0 = min(tid * per, p.B), s1 = min(s0 + per, p.B);
+  int cnt = 0, minctx = 0x7fffffff;
+  for (int sq = s0; sq < s1; ++sq) {
+    const SeqView v = seq_view(p, sq);
+    if (cascade_member(p, v)) {
+      ++cnt;
+      minctx = min(minctx, (int)clamp64(v.ctx, 0, v.kv_total));
+    }
+  }
+  // exclusive scan of the counts: within the wave by shuffles, then over the 4 wave sums
+  const int lane = tid & 63, wv = tid >> 6;
+  int incl = cnt;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) s_wsum[wv] = incl;
+  __syncthreads();
+  int nd = 0, k = incl - cnt;
+#pragma unroll
+  for (int w = 0; w < kPlanThreads / 64; ++w) {
+    const int ws = s_wsum[w];
+    nd += ws;
+    if (w < wv) k += ws;
+  }
+  for (int sq = s0; sq < s1; ++sq) {
+    if (cascade_member(p, seq_view(p, sq))) {
+      p.ws_dec_list[k] = sq;
+      if (k < kShareLdsList) s_list[k] = sq;
+      ++k;
+    }
+  }
+  minctx = block_min(minctx, red);  // its barriers make the list visible to the workgroup
+  int shared_tok = 0, r0 = 0;
+  if (nd >= 2 && minctx >= kCascadeMinChunks * kChunk) {
+    r0 = s_list[0];
+    const int64_t* t0 = p.bt + (int64_t)r0 * p.bt_rs;
+    const int jmax = min((minctx + p.BS - 1) / p.BS, p.W);
+    int first_bad = jmax;
+    // columns j0 + 256 c + tid (c < kShareCols) per pass; every load of a pass is independent,
+    // kShareRows members x kShareCols columns in flight per thread
+    for (int j0 = 0; j0 < jmax; j0 += kPlanThreads * kShareCols) {
+      int64_t ref[kShareCols];
+      bool ok[kShareCols];
+#pragma unroll
+      for (int c = 0; c < kShareCols; ++c) {
+        const int j = j0 + kPlanThreads * c + tid;
+        ref[c] = j < jmax ? t0[j] : 0;
+      }
+#pragma unroll
+      for (int c = 0; c < kShareCols; ++c) {
+        const int j = j0 + kPlanThreads * c + tid;
+        ok[c] = j >= jmax || (ref[c] >= 0 && ref[c] < p.num_blocks);
+      }
+      for (int m = 1; m < nd; m += kShareRows) {
+        int64_t row[kShareRows];
+#pragma unroll
+        for (int u = 0; u < kShareRows; ++u) {
+          const int mm = m + u;
+          const int sq = mm >= nd ? r0 : (mm < kShareLdsList ? s_list[mm] : p.ws_dec_list[mm]);
+          row[u] = (int64_t)sq * p.bt_rs;
+        }
+        int64_t v[kShareCols][kShareRows];
+#pragma unroll
+        for (int c = 0; c < kShareCols; ++c) {
+          const int j = j0 + kPlanThreads * c + tid;
+#pragma unroll
+          for (int u = 0; u < kShareRows; ++u) v[c][u] = j < jmax ? p.bt[row[u] + j] : 0;
+        }
+#pragma unroll
+        for (int c = 0; c < kShareCols; ++c)
+#pragma unroll
+          for (int u = 0; u < kShareRows; ++u) ok[c] = ok[c] && (v[c][u] == ref[c] || j0 + kPlanThreads * c + tid >= jmax);
+      }
+      int bad = jmax;
+#pragma unroll
+      for (int c = kShareCols - 1; c >= 0; --c)
+        if (!ok[c]) bad = j0 + kPlanThreads * c + tid;
+      first_bad = block_min(bad, red);
+      if (first_bad < jmax) break;  // workgroup-uniform
+    }
+    shared_tok = (int)min((int64_t)first_bad * p.BS, (int64_t)minctx) / kChunk * kChunk;
+    if (shared_tok < kCascadeMinChunks * kChunk) shared_tok = 0;
+  }
+  if (tid == 0) {
+    p.ws_share[0] = shared_tok;
+    p.ws_share[1] = (nd + p.SG - 1) / p.SG;
+    p.ws_share[2] = r0;
+    p.ws_share[3] = nd;
+  }
+}
+
+// Q rows of a prefix group: row n of the 16-row tile is member n / RS of group grp (its
+// decode-list index grp SG + n / RS), row n % RS of that sequence; every valid row sees all
+// L shared keys. Same k-slot order as load_q.
+template <int D, bool KV8>
+__device__ __forceinline__ void load_q_group(WaveState<D, 1>& s, const PAParams& p, int grp, int nd, int L,
+                                             int kvh) {
+  const int lane = threadIdx.x & 63;
+  const int j = lane >> 4, n = lane & 15;
+  s.m[0] = -INFINITY;
+  s.l[0] = 0.f;
+  s.thr[0] = -INFINITY;
+  s.nsh[0] = 0.f;
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) s.acc[0][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int mem = n / p.RS, rr = n % p.RS;
+  const int idx = grp * p.SG + mem;
+  bool valid = mem < p.SG && idx < nd;
+  const int seq = valid ? p.ws_dec_list[idx] : 0;
+  const SeqView sv = seq_view(p, seq);
+  const int qi = rr / p.G, g = rr % p.G;
+  valid = valid && qi < sv.q_len;
+  if (valid) {
+    const uint16_t* qp = (const uint16_t*)p.q + (sv.qs + qi) * p.q_ts + (int64_t)(kvh * p.G + g) * p.q_hs;
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+      const int d0 = KV8 ? 64 * (c >> 1) + 16 * j + 8 * (c & 1) : 32 * c + 8 * j;
+      s.q[0][c] = *(const u32x4*)(qp + d0);
+    }
+    s.limit[0] = L;
+  } else {
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) s.q[0][c] = u32x4{0, 0, 0, 0};
+    s.limit[0] = 0;
+  }
+}
+
+__device__ __forceinline__ void write_job_x(int32_t* job, int pieces, int64_t slot0, int64_t qs, int R, int kvh0,
+                                            int xpieces, int64_t xslot0, int xrow) {
+  job[1] = pieces;
+  job[2] = (int32_t)slot0;
+  job[3] = (int32_t)slot0;
+  job[4] = 1;
+  job[5] = (int32_t)qs;
+  job[6] = R;
+  job[7] = 0;
+  job[8] = kvh0;
+  job[9] = xpieces;
+  job[10] = (int32_t)xslot0;
+  job[11] = xrow;
+  job[0] = kJobDecode;
+}
 
 // Decode class: grid (NU * HGW / 4) workgroups of 4 waves; wave w of workgroup b is head
 // w % HGW of unit (4 b + w) / HGW. In mixed batches (PLAN) workgroup 0 computes the prefill
@@ -729,32 +934,68 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
   const bool job_writer = hw == 0 && lane == 0 && unit < p.NU;
   if (job_writer) job[0] = kJobNone;
 
+  // Cascade: keys [0, L) of every decode-class sequence come from the prefix segments, which
+  // take the first P = groups * NHG * L / 32 positions of the flat space.
+  int L = 0, ngrp = 0, r0 = 0, nd = 0;
+  if constexpr (NT == 1) {
+    if (p.CASC) {
+      L = (int)uni64(p.ws_share[0]);
+      ngrp = (int)uni64(p.ws_share[1]);
+      r0 = (int)uni64(p.ws_share[2]);
+      nd = (int)uni64(p.ws_share[3]);
+    }
+  }
+  const int Lc = L / kChunk;
+  const int64_t P = L > 0 ? (int64_t)ngrp * NHG * Lc : 0;
+
   // Chunks per segment over all sequences (every wave computes the sum itself).
-  int Cs = 0;
+  int Cs = 0, Ns = 0;
   for (int blk0 = 0; blk0 < p.B; blk0 += 64) {
     SeqWindow sw;
-    scan_window(sw, p, blk0, Cs);
+    scan_window(sw, p, blk0, Cs, Ns, L);
     Cs += sw.total;
+    Ns += sw.ntotal;
   }
-  const int64_t C = (int64_t)Cs * NHG;
+  const int64_t C = P + (int64_t)Cs * NHG;
   const int64_t NUa = active_units(C, p.NU);
   if (unit >= NUa) return;
   const int64_t a = unit * C / NUa, b = (unit + 1) * C / NUa;
   if (a >= b) return;
 
-  // walk the segments overlapping [a, b)
-  SeqWindow sw;
-  scan_window(sw, p, 0, 0);
   int64_t pos = a;
+  if constexpr (NT == 1) {
+    // prefix segments (g, hg): the 16-row tile of group g against keys [0, L) of head group hg,
+    // read through the first sequence's table (the shared blocks); always partial
+    while (pos < b && pos < P) {
+      const int64_t pseg = pos / Lc;
+      const int grp = (int)(pseg / NHG), hg = (int)(pseg % NHG);
+      const int64_t seg_beg = pseg * Lc, seg_end = seg_beg + Lc;
+      const int64_t y = b < seg_end ? b : seg_end;
+      const int kvh = hg * p.HGW + hw;
+      WaveState<D, 1> st;
+      load_q_group<D, KV8>(st, p, grp, nd, L, kvh);
+      const int64_t* btrow = p.bt + (int64_t)r0 * p.bt_rs;
+      run_chunks<E, D, 1, KV8>(st, p, btrow, kvh, (int)(pos - seg_beg) * kChunk, kChunk, (int)(y - seg_beg) * kChunk,
+                               L);  // fmt: skip
+      SeqView none{};
+      write_rows<E, D, 1>(st, p, none, 16, 0, kvh, true, p.ws_xacc, p.ws_xml, ((pseg + unit) * p.HGW + hw) * 16);
+      pos = y;
+    }
+  }
+
+  // walk the segments overlapping [a, b) (positions past the prefix region)
+  SeqWindow sw;
+  scan_window(sw, p, 0, 0, 0, L);
   while (pos < b) {
-    while ((int64_t)(sw.base + sw.total) * NHG <= pos) scan_window(sw, p, sw.blk0 + 64, sw.base + sw.total);
-    const int64_t start = (int64_t)(sw.base + sw.excl) * NHG;  // first chunk of this lane's sequence
+    while (P + (int64_t)(sw.base + sw.total) * NHG <= pos)
+      scan_window(sw, p, sw.blk0 + 64, sw.base + sw.total, sw.nbase + sw.ntotal, L);
+    const int64_t start = P + (int64_t)(sw.base + sw.excl) * NHG;  // first chunk of this lane's sequence
     const uint64_t hit = __builtin_amdgcn_ballot_w64(sw.c > 0 && start <= pos && pos < start + (int64_t)sw.c * NHG);
     if (hit == 0) break;  // cannot happen for consistent metadata; never index lane 64
     const int l = __builtin_ctzll(hit);
     const int seq = sw.blk0 + l;
     const int c = __builtin_amdgcn_readlane(sw.c, l);
-    const int64_t seq_start = (int64_t)(sw.base + __builtin_amdgcn_readlane(sw.excl, l)) * NHG;
+    const int64_t seq_start = P + (int64_t)(sw.base + __builtin_amdgcn_readlane(sw.excl, l)) * NHG;
     const int hg = (int)((pos - seq_start) / c);
     const int64_t seg_beg = seq_start + (int64_t)hg * c, seg_end = seg_beg + c;
     const int64_t y = b < seg_end ? b : seg_end;
@@ -762,16 +1003,39 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
 
     const SeqView sv = seq_view(p, seq);
     const int R = sv.q_len * p.G;
-    const int tok_lo = (int)(pos - seg_beg) * kChunk;
-    const int tok_hi = min((int)(y - seg_beg) * kChunk, sv.kv_total);
+    const bool member = L > 0 && __builtin_amdgcn_readlane(sw.mem, l);
+    const int skip = member ? L : 0;
+    const int tok_lo = skip + (int)(pos - seg_beg) * kChunk;
+    const int tok_hi = min(skip + (int)(y - seg_beg) * kChunk, sv.kv_total);
     WaveState<D, NT> st;
     load_q<D, NT, KV8>(st, p, sv.qs, R, 0, kvh, sv.ctx, sv.kv_total);
     const int64_t* btrow = p.bt + (int64_t)seq * p.bt_rs;
     run_chunks<E, D, NT, KV8>(st, p, btrow, kvh, tok_lo, kChunk, tok_hi, sv.kv_total);
-    const bool whole = pos == seg_beg && y == seg_end;
+    const bool whole = pos == seg_beg && y == seg_end && !member;
     const int64_t slot = (int64_t)seq * NHG + hg + unit;
     write_rows<E, D, NT>(st, p, sv, R, 0, kvh, !whole, p.ws_acc, p.ws_ml, (slot * p.HGW + hw) * p.RS);
-    if (job_writer && pos == seg_beg && y < seg_end) {
+    if (L > 0) {
+      if (hw == 0 && lane == 0 && pos == seg_beg) {
+        // one record per (seq, hg), written on every call: none for a whole segment; else the
+        // segment's own pieces in slot + i (units unit .. u1) and, for a member, the prefix
+        // segment (grp, hg)'s in pseg + uf + i (units uf .. ul), rows xrow .. of its tiles
+        int32_t* xj = p.ws_xjob + ((int64_t)seq * NHG + hg) * kJobInts;
+        const int64_t u1 = (seg_end * NUa - 1) / C;
+        if (whole) {
+          xj[0] = kJobNone;
+        } else if (member) {
+          const int idx = sw.nbase + __builtin_amdgcn_readlane(sw.nexcl, l);
+          const int grp = idx / p.SG, mem = idx % p.SG;
+          const int64_t pseg = (int64_t)grp * NHG + hg;
+          const int64_t x0 = pseg * Lc, x1 = x0 + Lc - 1;
+          const int64_t uf = ((x0 + 1) * NUa - 1) / C, ul = ((x1 + 1) * NUa - 1) / C;
+          write_job_x(xj, (int)(u1 - unit + 1), slot, sv.qs, R, hg * p.HGW, (int)(ul - uf + 1), pseg + uf,
+                      mem * p.RS);
+        } else {
+          write_job_x(xj, (int)(u1 - unit + 1), slot, sv.qs, R, hg * p.HGW, 0, 0, 0);
+        }
+      }
+    } else if (job_writer && pos == seg_beg && y < seg_end) {
       // the segment starts here and continues in units unit + 1 .. u1: piece i is in slot + i
       const int64_t u1 = (seg_end * NUa - 1) / C;
       write_job(job, kJobDecode, (int)(u1 - unit + 1), slot, slot, 1, sv.qs, R, 0, hg * p.HGW);
@@ -803,17 +1067,28 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
   __shared__ float s_inv[kMergeRows];
   const int CD = merge_chunks_decode(p);
   const int b = blockIdx.x;
-  int64_t jidx;
   int chunk;
-  if (b < p.NU * CD) {
-    jidx = b / CD;
+  const int32_t* job;
+  bool casc = false;
+  if (p.CASC && p.ws_share[0] > 0) {
+    // cascade: one record per (sequence, head group), written for decode-class sequences
+    const int NHG = p.Hkv / p.HGW;
+    if (b >= p.B * NHG * CD) return;
+    const int seg = b / CD;
+    chunk = b % CD;
+    const SeqView v = seq_view(p, seg / NHG);
+    if (v.q_len == 0 || v.q_len > p.QS) return;
+    job = p.ws_xjob + (int64_t)seg * kJobInts;
+    casc = true;
+  } else if (b < p.NU * CD) {
+    job = p.ws_job + (int64_t)(b / CD) * kJobInts;
     chunk = b % CD;
   } else {
     const int bp = b - p.NU * CD;
-    jidx = (int64_t)kMaxDecodeWaves + bp / (kPrefillRows / kMergeRows);
+    if (bp >= p.NUP * (kPrefillRows / kMergeRows)) return;  // grid sized for the cascade records
+    job = p.ws_job + ((int64_t)kMaxDecodeWaves + bp / (kPrefillRows / kMergeRows)) * kJobInts;
     chunk = bp % (kPrefillRows / kMergeRows);
   }
-  const int32_t* job = p.ws_job + jidx * kJobInts;
   const int kind = job[0];
   if (kind == kJobNone) return;
   const bool dec = kind == kJobDecode;
@@ -829,14 +1104,28 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
   const int rph = dec ? p.RS : kPrefillRows;  // rows per head
   const float* acc = dec ? p.ws_acc : p.ws_pacc;
   const float* ml = dec ? p.ws_ml : p.ws_pml;
-  auto slot = [&](int i) -> int64_t { return i == 0 ? slot0 : slotb + (int64_t)stride * i; };
+  // Two piece sets: 0 = the job's own partials, row x of piece i at base(0, i) + x; 1 (cascade)
+  // = the prefix segment's, row x (head x / RS, row x % RS) at row xrow + x % RS of that head's
+  // 16-row tile, base(1, i) = (xslot0 + i) HGW 16.
+  const int xpieces = casc ? job[9] : 0;
+  const int64_t xslot0 = casc ? job[10] : 0;
+  const int xrow = casc ? job[11] : 0;
+  auto roff = [&](int set, int x) -> int64_t { return set == 0 ? x : (x / rph) * 16 + xrow + x % rph; };
+  auto base = [&](int set, int i) -> int64_t {
+    return set == 0 ? (i == 0 ? slot0 : slotb + (int64_t)stride * i) * rows : (xslot0 + i) * p.HGW * 16;
+  };
+  const int nsets = xpieces > 0 ? 2 : 1;
   const int t = threadIdx.x;
 
   float msafe = 0.f, L = 0.f;
   if (t < nr) {
     float M = -INFINITY;
+    for (int set = 0; set < nsets; ++set) {
+      const int n = set ? xpieces : pieces;
+      const float* mp = (set ? p.ws_xml : ml) + roff(set, x0 + t) * 2;
 #pragma unroll 8
-    for (int i = 0; i < pieces; ++i) M = fmaxf(M, ml[(slot(i) * rows + x0 + t) * 2]);
+      for (int i = 0; i < n; ++i) M = fmaxf(M, mp[base(set, i) * 2]);
+    }
     msafe = M == -INFINITY ? 0.f : M;
   }
   const int nq = nr * Q4;
@@ -846,28 +1135,36 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
   f32x4 o[F];
 #pragma unroll
   for (int f = 0; f < F; ++f) o[f] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int i0 = 0; i0 < pieces; i0 += kMergeBatch) {
-    __syncthreads();
-    if (t < nr) {
+  for (int set = 0; set < nsets; ++set) {
+    const int n = set ? xpieces : pieces;
+    const float* ap = set ? p.ws_xacc : acc;
+    const float* mp = (set ? p.ws_xml : ml) + (t < nr ? roff(set, x0 + t) : 0) * 2;
+    int64_t rf[F];  // this thread's float4 of piece 0 (relative to the piece base)
 #pragma unroll
-      for (int k = 0; k < kMergeBatch; ++k) {
-        const int i = i0 + k;
-        float w = 0.f;
-        if (i < pieces) {
-          const float2 x = *(const float2*)(ml + (slot(i) * rows + x0 + t) * 2);
-          w = fast_exp2(x.x - msafe);
-          L += w * x.y;
+    for (int f = 0; f < F; ++f) rf[f] = roff(set, x0 + qc[f] / Q4) * D + 4 * (qc[f] % Q4);
+    for (int i0 = 0; i0 < n; i0 += kMergeBatch) {
+      __syncthreads();
+      if (t < nr) {
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; ++k) {
+          const int i = i0 + k;
+          float w = 0.f;
+          if (i < n) {
+            const float2 x = *(const float2*)(mp + base(set, i) * 2);
+            w = fast_exp2(x.x - msafe);
+            L += w * x.y;
+          }
+          s_w[t][k] = w;
         }
-        s_w[t][k] = w;
       }
-    }
-    __syncthreads();
-    const int ni = min(kMergeBatch, pieces - i0);
-#pragma unroll 4
-    for (int k = 0; k < ni; ++k) {
-      const float* src = acc + (slot(i0 + k) * rows + x0) * D;
+      __syncthreads();
+      const int ni = min(kMergeBatch, n - i0);
+#pragma unroll 8
+      for (int k = 0; k < ni; ++k) {
+        const float* src = ap + base(set, i0 + k) * D;
 #pragma unroll
-      for (int f = 0; f < F; ++f) o[f] += s_w[qc[f] / Q4][k] * *(const f32x4*)(src + 4 * qc[f]);
+        for (int f = 0; f < F; ++f) o[f] += s_w[qc[f] / Q4][k] * *(const f32x4*)(src + rf[f]);
+      }
     }
   }
   if (t < nr) s_inv[t] = p.v_scale / (L == 0.f ? 1.f : L);
@@ -1738,6 +2035,12 @@ template <class E, int D, bool KV8>
 static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipStream_t s, LaunchLog& log) {
   int err = 0;
   p.PLAN = plan.launch_prefill ? 1 : 0;
+  p.CASC = plan.cascade ? 1 : 0;
+  if (plan.cascade) {
+    hipLaunchKernelGGL(pa_share_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
+    if ((err = (int)hipGetLastError())) return err;
+    log.after_launch(5, s);
+  }
   if (plan.launch_prefill) {
     // the unit count is fixed before the decode launch: both kernels write merge jobs
     int units = resident_blocks((const void*)&pa_prefill_kernel<E, D, KV8>);
@@ -1760,7 +2063,8 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipSt
     log.after_launch(2, s);
   }
   const int cd = (p.HGW * p.RS + kMergeRows - 1) / kMergeRows;
-  const dim3 mg(p.NU * cd + p.NUP * (kPrefillRows / kMergeRows));
+  const int nseg = plan.cascade ? p.B * (p.Hkv / p.HGW) : 0;  // cascade records
+  const dim3 mg((p.NU > nseg ? p.NU : nseg) * cd + p.NUP * (kPrefillRows / kMergeRows));
   hipLaunchKernelGGL((pa_merge_kernel<E, D>), mg, dim3(256), 0, s, p);
   if ((err = (int)hipGetLastError())) return err;
   log.after_launch(3, s);

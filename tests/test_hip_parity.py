@@ -100,6 +100,8 @@ def test_baseline_configs(hip_device, idx):
         err = pc.max_err_vs_oracle(b, out, seqs)
     print(f"config {idx}: max abs err vs fp64 oracle {err:.3e}; kernels {last_launch_kernels()}")
     assert err <= pc.TOL_16BIT, err
+    if idx == 4:  # the 750 shared blocks go through the cascade's prefix segments
+        assert last_launch_kernels()[0] == "share"
 
 
 def test_out_argument_and_strided_inputs(hip_device):
