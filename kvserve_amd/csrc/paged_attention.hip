@@ -1048,11 +1048,10 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
 // heads x RS rows for decode, kPrefillRows rows of one head for prefill); row x of piece i
 // sits at (slot(i) * rows + x) in the partial arrays. Each workgroup merges 16 rows of one
 // job: workgroups 0 .. NU * CD - 1 take decode unit b / CD, rows 16 (b % CD) ..; the next
-// NUP * 8 take prefill record b' / 8, rows 16 (b' % 8) ... Thread t < 16 finds the max of
-// its row over the pieces and stages the pieces' weights in LDS, 16 pieces at a time; then
-// every thread accumulates F = D / 64 float4 of the 16 rows with the piece loop unrolled,
-// so the loads of several pieces are in flight together. Rows are normalised at the store.
-constexpr int kMergeBatch = 16;
+// NUP * 8 take prefill record b' / 8, rows 16 (b' % 8) ... Every thread owns F = D / 64
+// float4 of the 16 rows and merges them online over the pieces, kMergeBatch pieces per
+// round of loads. Rows are normalised at the store.
+constexpr int kMergeBatch = 8;
 constexpr int kMergeRows = 16;
 
 __device__ __forceinline__ int merge_chunks_decode(const PAParams& p) {
@@ -1063,8 +1062,6 @@ template <class E, int D>
 __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
   constexpr int Q4 = D / 4;                    // float4 per row
   constexpr int F = kMergeRows * Q4 / 256;     // float4 per thread
-  __shared__ float s_w[kMergeRows][kMergeBatch + 1];
-  __shared__ float s_inv[kMergeRows];
   const int CD = merge_chunks_decode(p);
   const int b = blockIdx.x;
   int chunk;
@@ -1093,15 +1090,19 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
   if (kind == kJobNone) return;
   const bool dec = kind == kJobDecode;
   const int rows = dec ? p.HGW * p.RS : kPrefillRows;
-  const int x0 = chunk * kMergeRows;
-  if (x0 >= rows) return;
-  const int nr = min(kMergeRows, rows - x0);
   const int pieces = job[1];
   const int64_t slot0 = job[2], slotb = job[3];
   const int stride = job[4];
   const int64_t qs = job[5];
   const int R = job[6], rbase = job[7], kvh0 = job[8];
   const int rph = dec ? p.RS : kPrefillRows;  // rows per head
+  // only the rows that reach the output: rv = min(rph, R - rbase) of each head's rph; the
+  // workgroup's 16 are valid rows x0 .. x0 + 15, valid row v being piece row (v / rv) rph + v % rv
+  const int rv = min(rph, R - rbase);
+  const int x0 = chunk * kMergeRows;
+  if (rv <= 0 || x0 >= (rows / rph) * rv) return;
+  const int nr = min(kMergeRows, (rows / rph) * rv - x0);
+  auto prow = [&](int v) { return (v / rv) * rph + v % rv; };
   const float* acc = dec ? p.ws_acc : p.ws_pacc;
   const float* ml = dec ? p.ws_ml : p.ws_pml;
   // Two piece sets: 0 = the job's own partials, row x of piece i at base(0, i) + x; 1 (cascade)
@@ -1116,68 +1117,80 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
   };
   const int nsets = xpieces > 0 ? 2 : 1;
   const int t = threadIdx.x;
-
-  float msafe = 0.f, L = 0.f;
-  if (t < nr) {
-    float M = -INFINITY;
-    for (int set = 0; set < nsets; ++set) {
-      const int n = set ? xpieces : pieces;
-      const float* mp = (set ? p.ws_xml : ml) + roff(set, x0 + t) * 2;
-#pragma unroll 8
-      for (int i = 0; i < n; ++i) M = fmaxf(M, mp[base(set, i) * 2]);
-    }
-    msafe = M == -INFINITY ? 0.f : M;
-  }
   const int nq = nr * Q4;
   int qc[F];
 #pragma unroll
   for (int f = 0; f < F; ++f) qc[f] = min(t + 256 * f, nq - 1);  // clamped: loads stay in the rows
+
+  // Online merge: kMergeBatch pieces at a time, every load of a batch (the m/l pair of each
+  // float4's row and the float4) issued before any is used; the running max M moves per batch.
   f32x4 o[F];
+  float M[F], Ls[F];
 #pragma unroll
-  for (int f = 0; f < F; ++f) o[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int f = 0; f < F; ++f) {
+    o[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+    M[f] = -INFINITY;
+    Ls[f] = 0.f;
+  }
   for (int set = 0; set < nsets; ++set) {
     const int n = set ? xpieces : pieces;
     const float* ap = set ? p.ws_xacc : acc;
-    const float* mp = (set ? p.ws_xml : ml) + (t < nr ? roff(set, x0 + t) : 0) * 2;
-    int64_t rf[F];  // this thread's float4 of piece 0 (relative to the piece base)
+    const float* mp = set ? p.ws_xml : ml;
+    int64_t rr[F];  // this thread's rows relative to the piece base
 #pragma unroll
-    for (int f = 0; f < F; ++f) rf[f] = roff(set, x0 + qc[f] / Q4) * D + 4 * (qc[f] % Q4);
-    for (int i0 = 0; i0 < n; i0 += kMergeBatch) {
-      __syncthreads();
-      if (t < nr) {
+    for (int f = 0; f < F; ++f) rr[f] = roff(set, prow(x0 + qc[f] / Q4));
+    auto batch = [&](int i0, auto kb) {
+      constexpr int KB = decltype(kb)::value;
+      float2 mv[KB][F];
+      f32x4 av[KB][F];
 #pragma unroll
-        for (int k = 0; k < kMergeBatch; ++k) {
-          const int i = i0 + k;
-          float w = 0.f;
-          if (i < n) {
-            const float2 x = *(const float2*)(mp + base(set, i) * 2);
-            w = fast_exp2(x.x - msafe);
-            L += w * x.y;
-          }
-          s_w[t][k] = w;
+      for (int k = 0; k < KB; ++k) {
+        const int64_t bk = base(set, min(i0 + k, n - 1));
+#pragma unroll
+        for (int f = 0; f < F; ++f) {
+          mv[k][f] = *(const float2*)(mp + (bk + rr[f]) * 2);
+          av[k][f] = *(const f32x4*)(ap + (bk + rr[f]) * D + 4 * (qc[f] % Q4));
         }
       }
-      __syncthreads();
-      const int ni = min(kMergeBatch, n - i0);
-#pragma unroll 8
-      for (int k = 0; k < ni; ++k) {
-        const float* src = ap + base(set, i0 + k) * D;
 #pragma unroll
-        for (int f = 0; f < F; ++f) o[f] += s_w[qc[f] / Q4][k] * *(const f32x4*)(src + rf[f]);
+      for (int f = 0; f < F; ++f) {
+        float mb = M[f];
+#pragma unroll
+        for (int k = 0; k < KB; ++k) mb = i0 + k < n ? fmaxf(mb, mv[k][f].x) : mb;
+        const float ms = mb == -INFINITY ? 0.f : mb;  // all -inf so far: every weight is 0
+        const float alpha = fast_exp2(M[f] - ms);
+        o[f] *= alpha;
+        Ls[f] *= alpha;
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+          const float w = i0 + k < n ? fast_exp2(mv[k][f].x - ms) : 0.f;
+          Ls[f] += w * mv[k][f].y;
+          o[f] += w * av[k][f];
+        }
+        M[f] = mb;
       }
+    };
+    // batches of 8 pieces, the rest as 4 + 2 + 1: no load is issued for a missing piece
+    int i0 = 0;
+    for (; n - i0 >= kMergeBatch; i0 += kMergeBatch) batch(i0, std::integral_constant<int, kMergeBatch>{});
+    if (n - i0 >= 4) {
+      batch(i0, std::integral_constant<int, 4>{});
+      i0 += 4;
     }
+    if (n - i0 >= 2) {
+      batch(i0, std::integral_constant<int, 2>{});
+      i0 += 2;
+    }
+    if (n - i0 >= 1) batch(i0, std::integral_constant<int, 1>{});
   }
-  if (t < nr) s_inv[t] = p.v_scale / (L == 0.f ? 1.f : L);
-  __syncthreads();
 #pragma unroll
   for (int f = 0; f < F; ++f) {
     const int q = t + 256 * f;
     if (q >= nq) continue;
     const int xr = q / Q4, col = 4 * (q % Q4);
-    const int x = x0 + xr;
+    const int x = prow(x0 + xr);
     const int hw = x / rph, r = rbase + x % rph;
-    if (r >= R) continue;
-    const float inv = s_inv[xr];
+    const float inv = p.v_scale / (Ls[f] == 0.f ? 1.f : Ls[f]);
     uint16_t* dst = (uint16_t*)p.out + (qs + r / p.G) * p.o_ts + (int64_t)((kvh0 + hw) * p.G + r % p.G) * p.o_hs + col;
     *(u32x2*)dst = u32x2{E::pack2(o[f][0] * inv, o[f][1] * inv), E::pack2(o[f][2] * inv, o[f][3] * inv)};
   }
