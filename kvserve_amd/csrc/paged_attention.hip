@@ -760,7 +760,7 @@ __device__ __forceinline__ int block_min(int v, int* red) {
 
 constexpr int kShareLdsList = 1024;  // members whose ids stay in LDS for the column compare
 constexpr int kShareCols = 4;        // columns per thread and pass
-constexpr int kShareRows = 8;        // member rows loaded together
+constexpr int kShareRows = 16;       // member rows loaded together
 
 __global__ __launch_bounds__(kPlanThreads) void pa_share_kernel(PAParams p) {
   __shared__ int s_wsum[kPlanThreads / 64];
@@ -811,19 +811,12 @@ __global__ __launch_bounds__(kPlanThreads) void pa_share_kernel(PAParams p) {
     // columns j0 + 256 c + tid (c < kShareCols) per pass; every load of a pass is independent,
     // kShareRows members x kShareCols columns in flight per thread
     for (int j0 = 0; j0 < jmax; j0 += kPlanThreads * kShareCols) {
-      int64_t ref[kShareCols];
       bool ok[kShareCols];
+      int64_t ref[kShareCols];
 #pragma unroll
-      for (int c = 0; c < kShareCols; ++c) {
-        const int j = j0 + kPlanThreads * c + tid;
-        ref[c] = j < jmax ? t0[j] : 0;
-      }
-#pragma unroll
-      for (int c = 0; c < kShareCols; ++c) {
-        const int j = j0 + kPlanThreads * c + tid;
-        ok[c] = j >= jmax || (ref[c] >= 0 && ref[c] < p.num_blocks);
-      }
+      for (int c = 0; c < kShareCols; ++c) ok[c] = true;
       for (int m = 1; m < nd; m += kShareRows) {
+        // the reference entries and kShareRows members' entries of this pass in one round of loads
         int64_t row[kShareRows];
 #pragma unroll
         for (int u = 0; u < kShareRows; ++u) {
@@ -835,13 +828,19 @@ __global__ __launch_bounds__(kPlanThreads) void pa_share_kernel(PAParams p) {
 #pragma unroll
         for (int c = 0; c < kShareCols; ++c) {
           const int j = j0 + kPlanThreads * c + tid;
+          ref[c] = j < jmax ? t0[j] : 0;
 #pragma unroll
           for (int u = 0; u < kShareRows; ++u) v[c][u] = j < jmax ? p.bt[row[u] + j] : 0;
         }
 #pragma unroll
         for (int c = 0; c < kShareCols; ++c)
 #pragma unroll
-          for (int u = 0; u < kShareRows; ++u) ok[c] = ok[c] && (v[c][u] == ref[c] || j0 + kPlanThreads * c + tid >= jmax);
+          for (int u = 0; u < kShareRows; ++u) ok[c] = ok[c] && v[c][u] == ref[c];
+      }
+#pragma unroll
+      for (int c = 0; c < kShareCols; ++c) {
+        const int j = j0 + kPlanThreads * c + tid;
+        ok[c] = j >= jmax || (ok[c] && ref[c] >= 0 && ref[c] < p.num_blocks);
       }
       int bad = jmax;
 #pragma unroll
