@@ -79,6 +79,22 @@ def test_shared_prefix_matches_oracle(hip_device, name):
     print(f"{name}: {kinds} err {err:.3e}")
 
 
+def test_members_numbered_across_scan_windows(hip_device):
+    """150 sequences (three 64-sequence scan windows of the decode kernel, several sequences
+    per thread in the share kernel), non-members spread over all windows: each member's group
+    and row in the prefix tiles come from its number among the members, counted across windows."""
+    rng = random.Random(21)
+    q = [1] * 150
+    ctx = [rng.randint(300, 2500) if i % 7 else rng.randint(20, 250) for i in range(150)]
+    w = shared_workload(q, ctx, (32, 8), 128, 16, 18, 600, seed=21)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=21)
+    out = pc.attend(b)
+    assert last_launch_kernels()[0] == "share"
+    seqs = list(range(0, 150, 3)) + [149]
+    err = pc.max_err_vs_oracle(b, out, seqs)
+    assert err <= pc.TOL_16BIT, err
+
+
 def test_padding_rows_and_short_contexts_stay_out(hip_device):
     """Graph padding rows (seq_len 1, tables of one scratch block) and sequences with under
     256 context tokens are not members; the members still share their prefix."""
