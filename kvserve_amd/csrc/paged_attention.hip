@@ -1045,46 +1045,32 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
 
 // Log-sum-exp merge of split segments. A job covers `rows` partial rows per piece (HGW
 // heads x RS rows for decode, kPrefillRows rows of one head for prefill); row x of piece i
-// sits at (slot(i) * rows + x) in the partial arrays. Each workgroup merges 16 rows of one
-// job: workgroups 0 .. NU * CD - 1 take decode unit b / CD, rows 16 (b % CD) ..; the next
-// NUP * 8 take prefill record b' / 8, rows 16 (b' % 8) ... Every thread owns F = D / 64
-// float4 of the 16 rows and merges them online over the pieces, kMergeBatch pieces per
-// round of loads. Rows are normalised at the store.
-constexpr int kMergeBatch = 8;
-constexpr int kMergeRows = 16;
-
-__device__ __forceinline__ int merge_chunks_decode(const PAParams& p) {
-  return (p.HGW * p.RS + kMergeRows - 1) / kMergeRows;
+// sits at (slot(i) * rows + x) in the partial arrays. Each workgroup merges MR = 1024 / D
+// rows of one job: workgroups 0 .. NU * CD - 1 take decode unit b / CD, rows MR (b % CD) ..;
+// the next NUP * (128 / MR) take prefill record b' / (128 / MR), rows MR (b' % (128 / MR)) ...
+// Every thread owns one float4 of the MR rows and merges it online over the pieces,
+// kMergeBatch pieces per round of loads. Rows are normalised at the store.
+constexpr int kMergeBatch = 16;
+// rows per merge workgroup with F float4 of one row per thread: F 1024 / D (decode jobs
+// F = 1: 8 rows at D = 128; prefill jobs F = 2: 16 rows)
+template <int D, int F = 1>
+constexpr int merge_rows() {
+  return F * 256 * 4 / D;
 }
 
-template <class E, int D>
-__global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
-  constexpr int Q4 = D / 4;                    // float4 per row
-  constexpr int F = kMergeRows * Q4 / 256;     // float4 per thread
-  const int CD = merge_chunks_decode(p);
-  const int b = blockIdx.x;
-  int chunk;
-  const int32_t* job;
-  bool casc = false;
-  if (p.CASC && p.ws_share[0] > 0) {
-    // cascade: one record per (sequence, head group), written for decode-class sequences
-    const int NHG = p.Hkv / p.HGW;
-    if (b >= p.B * NHG * CD) return;
-    const int seg = b / CD;
-    chunk = b % CD;
-    const SeqView v = seq_view(p, seg / NHG);
-    if (v.q_len == 0 || v.q_len > p.QS) return;
-    job = p.ws_xjob + (int64_t)seg * kJobInts;
-    casc = true;
-  } else if (b < p.NU * CD) {
-    job = p.ws_job + (int64_t)(b / CD) * kJobInts;
-    chunk = b % CD;
-  } else {
-    const int bp = b - p.NU * CD;
-    if (bp >= p.NUP * (kPrefillRows / kMergeRows)) return;  // grid sized for the cascade records
-    job = p.ws_job + ((int64_t)kMaxDecodeWaves + bp / (kPrefillRows / kMergeRows)) * kJobInts;
-    chunk = bp % (kPrefillRows / kMergeRows);
-  }
+// F = 1 in decode-only batches; in mixed batches F = 2, since there a head's RS = 16 / G row
+// slots mostly hold a single query's G rows and the workgroups past them return at once
+template <int D, bool MIXED>
+constexpr int merge_rows_decode() {
+  return MIXED ? merge_rows<D, 2>() : merge_rows<D, 1>();
+}
+
+// One workgroup's share of a merge job: rows MR = F * 1024 / D of it (chunk), F float4 of
+// one row per thread.
+template <class E, int D, int F>
+__device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job, int chunk, bool casc) {
+  constexpr int Q4 = D / 4;  // float4 per row
+  constexpr int kMergeRows = merge_rows<D, F>();
   const int kind = job[0];
   if (kind == kJobNone) return;
   const bool dec = kind == kJobDecode;
@@ -1169,9 +1155,15 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
         M[f] = mb;
       }
     };
-    // batches of 8 pieces, the rest as 4 + 2 + 1: no load is issued for a missing piece
+    // batches of kMergeBatch / F pieces (16 float4 loads in flight per thread), the rest as
+    // 8 + 4 + 2 + 1: no load is issued for a missing piece
+    constexpr int KB = kMergeBatch / F;
     int i0 = 0;
-    for (; n - i0 >= kMergeBatch; i0 += kMergeBatch) batch(i0, std::integral_constant<int, kMergeBatch>{});
+    for (; n - i0 >= KB; i0 += KB) batch(i0, std::integral_constant<int, KB>{});
+    if (KB > 8 && n - i0 >= 8) {
+      batch(i0, std::integral_constant<int, 8>{});
+      i0 += 8;
+    }
     if (n - i0 >= 4) {
       batch(i0, std::integral_constant<int, 4>{});
       i0 += 4;
@@ -1193,6 +1185,40 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
     uint16_t* dst = (uint16_t*)p.out + (qs + r / p.G) * p.o_ts + (int64_t)((kvh0 + hw) * p.G + r % p.G) * p.o_hs + col;
     *(u32x2*)dst = u32x2{E::pack2(o[f][0] * inv, o[f][1] * inv), E::pack2(o[f][2] * inv, o[f][3] * inv)};
   }
+}
+
+// MIXED: the batch has prefill-class sequences (prefill records after the decode units);
+// decode and prefill jobs then both take 2 float4 per thread (16 rows at D = 128).
+template <class E, int D, bool MIXED>
+__global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
+  constexpr int F = MIXED ? 2 : 1;
+  constexpr int MR = merge_rows<D, F>();
+  const int CD = (p.HGW * p.RS + MR - 1) / MR;
+  const int b = blockIdx.x;
+  const int32_t* job;
+  int chunk;
+  bool casc = false;
+  if (p.CASC && p.ws_share[0] > 0) {
+    // cascade: one record per (sequence, head group), written for decode-class sequences
+    const int NHG = p.Hkv / p.HGW;
+    if (b >= p.B * NHG * CD) return;
+    const int seg = b / CD;
+    const SeqView v = seq_view(p, seg / NHG);
+    if (v.q_len == 0 || v.q_len > p.QS) return;
+    job = p.ws_xjob + (int64_t)seg * kJobInts;
+    chunk = b % CD;
+    casc = true;
+  } else if (b < p.NU * CD) {
+    job = p.ws_job + (int64_t)(b / CD) * kJobInts;
+    chunk = b % CD;
+  } else {
+    if constexpr (!MIXED) return;
+    const int bp = b - p.NU * CD;
+    if (bp >= p.NUP * (kPrefillRows / MR)) return;
+    job = p.ws_job + ((int64_t)kMaxDecodeWaves + bp / (kPrefillRows / MR)) * kJobInts;
+    chunk = bp % (kPrefillRows / MR);
+  }
+  merge_job<E, D, F>(p, job, chunk, casc);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -2074,10 +2100,14 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipSt
     if ((err = (int)hipGetLastError())) return err;
     log.after_launch(2, s);
   }
-  const int cd = (p.HGW * p.RS + kMergeRows - 1) / kMergeRows;
+  const int mr = plan.launch_prefill ? merge_rows_decode<D, true>() : merge_rows_decode<D, false>();
+  const int cd = (p.HGW * p.RS + mr - 1) / mr;
   const int nseg = plan.cascade ? p.B * (p.Hkv / p.HGW) : 0;  // cascade records
-  const dim3 mg((p.NU > nseg ? p.NU : nseg) * cd + p.NUP * (kPrefillRows / kMergeRows));
-  hipLaunchKernelGGL((pa_merge_kernel<E, D>), mg, dim3(256), 0, s, p);
+  const dim3 mg((p.NU > nseg ? p.NU : nseg) * cd + p.NUP * (kPrefillRows / merge_rows<D, 2>()));
+  if (plan.launch_prefill)
+    hipLaunchKernelGGL((pa_merge_kernel<E, D, true>), mg, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((pa_merge_kernel<E, D, false>), mg, dim3(256), 0, s, p);
   if ((err = (int)hipGetLastError())) return err;
   log.after_launch(3, s);
   return 0;
