@@ -665,7 +665,7 @@ __device__ __forceinline__ void write_job(int32_t* job, int kind, int pieces, in
 // waves of a unit take the HGW heads of each segment, so they stream adjacent slices of the
 // same cache rows. A segment split between units leaves one partial per unit in slot
 // (segment index + unit); the unit holding a split segment's first piece records a merge job.
-constexpr int kMinUnitChunks = 4;
+constexpr int kMinUnitChunks = 2;
 
 // A cascade member: a decode-class sequence with at least kCascadeMinChunks chunks of context
 // (so padding rows and short sequences never limit the shared length).
