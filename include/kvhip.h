@@ -254,6 +254,15 @@ KVH_API int kvh_silu_mul(const void* gate_up, int64_t gate_up_tok_stride, void* 
 KVH_API int kvh_gemv(const void* x, int64_t x_row_stride, const void* weight, int64_t w_row_stride,
                      void* y, int64_t y_row_stride, int32_t m, int32_t n, int32_t k, int32_t dtype, void* stream);
 
+/* gemv_silu_mul: the fused gate_up projection followed by silu_mul (model.py MLP,
+ * act(gate) * up of the chunked gate_up output), for m <= 4 rows: with g[i][j], u[i][j] the
+ * projections on weight rows j and inter + j (w_gate_up is [2 * inter, k] row-major), each
+ * rounded to dtype, y[i][j] = (silu(g).to(dtype) * u).to(dtype) -- the bits of kvh_gemv then
+ * kvh_silu_mul. k % 8 == 0. */
+KVH_API int kvh_gemv_silu_mul(const void* x, int64_t x_row_stride, const void* w_gate_up, int64_t w_row_stride,
+                              void* y, int64_t y_row_stride, int32_t m, int32_t inter, int32_t k, int32_t dtype,
+                              void* stream);
+
 /*
  * Launch-timing hook for benchmarks (no counterpart in the reference). When armed with an
  * array of n <= 8 hipEvent_t handles (created by the caller with timing enabled), the NEXT

@@ -10,6 +10,9 @@
 //   gemv:        y[m][n] = sum_k x[m][k] w[n][k] for m < M <= 8 (nn.Linear with a [N, K]
 //                weight), fp32 accumulation; HBM-bound on the weight, which each wave
 //                streams in 1 KB loads while x comes from L1/L2.
+//   gemv + silu_mul (GLU): the gate_up projection with silu_mul in its epilogue: a wave
+//                takes gate rows j .. and the up rows I + j .., rounds both sums to the
+//                storage type (the projection's output) and applies silu_mul's arithmetic.
 #include "kvh_device.h"
 #include "kvh_internal.h"
 
@@ -103,14 +106,29 @@ __global__ __launch_bounds__(kOpsThreads) void silu_mul_kernel(const uint16_t* _
 
 // GEMV: a wave owns RW consecutive weight rows and walks k in steps of 512 (64 lanes x 8
 // elements, one 16-byte load per lane per row), two steps per iteration so 2 RW weight loads
-// are in flight; lane partial sums are reduced across the wave at the end.
-template <class E, int M, int RW>
+// are in flight; lane partial sums are reduced across the wave at the end. Products are
+// accumulated with explicit FMAs (no two-product dot instructions), so a row's sum has the
+// same bits in every instantiation.
+// silu_mul of one (gate, up) pair of fp32 sums, each first rounded to the storage type
+template <class E>
+__device__ __forceinline__ float silu_mul1(float g, float u) {
+  g = E::to_f32((uint16_t)(E::pack2(g, 0.f) & 0xffffu));
+  u = E::to_f32((uint16_t)(E::pack2(u, 0.f) & 0xffffu));
+  g = g / (1.f + expf(-g));
+  g = E::to_f32((uint16_t)(E::pack2(g, 0.f) & 0xffffu));
+  return g * u;
+}
+
+// GLU: n is the intermediate size I; the weight has 2 I rows (gate, then up); wave rows
+// r < RW / 2 are gate rows n0 + r, the others up rows I + n0 + r - RW / 2, n0 = wave RW / 2.
+template <class E, int M, int RW, bool GLU = false>
 __global__ __launch_bounds__(kOpsThreads) void gemv_kernel(const uint16_t* __restrict__ x, int64_t x_rs,
                                                            const uint16_t* __restrict__ w, int64_t w_rs,
                                                            uint16_t* __restrict__ y, int64_t y_rs, int n, int k) {
+  constexpr int OUT = GLU ? RW / 2 : RW;  // outputs per wave
   const int lane = threadIdx.x & 63;
   const int wave = blockIdx.x * (kOpsThreads / 64) + (threadIdx.x >> 6);
-  const int n0 = wave * RW;
+  const int n0 = wave * OUT;
   if (n0 >= n) return;
   float acc[M][RW];
 #pragma unroll
@@ -119,7 +137,12 @@ __global__ __launch_bounds__(kOpsThreads) void gemv_kernel(const uint16_t* __res
     for (int r = 0; r < RW; ++r) acc[m][r] = 0.f;
   const uint16_t* wr[RW];
 #pragma unroll
-  for (int r = 0; r < RW; ++r) wr[r] = w + (int64_t)min(n0 + r, n - 1) * w_rs;  // rows past n repeat the last
+  for (int r = 0; r < RW; ++r) {
+    if constexpr (GLU)  // rows past n repeat the last gate / up row
+      wr[r] = w + ((int64_t)(r < OUT ? 0 : n) + min(n0 + r % OUT, n - 1)) * w_rs;
+    else
+      wr[r] = w + (int64_t)min(n0 + r, n - 1) * w_rs;  // rows past n repeat the last
+  }
   const int kfull = k / 1024 * 1024;
   for (int k0 = 8 * lane; k0 < kfull; k0 += 1024) {
     u32x4 wv[2][RW], xv[2][M];
@@ -141,7 +164,7 @@ __global__ __launch_bounds__(kOpsThreads) void gemv_kernel(const uint16_t* __res
           float wf[8];
           unpack8<E>(wv[s][r], wf);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[m][r] += xf[i] * wf[i];
+          for (int i = 0; i < 8; ++i) acc[m][r] = __builtin_fmaf(xf[i], wf[i], acc[m][r]);
         }
       }
   }
@@ -155,7 +178,7 @@ __global__ __launch_bounds__(kOpsThreads) void gemv_kernel(const uint16_t* __res
         float wf[8];
         unpack8<E>(*(const u32x4*)(wr[r] + k0), wf);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[m][r] += xf[i] * wf[i];
+        for (int i = 0; i < 8; ++i) acc[m][r] = __builtin_fmaf(xf[i], wf[i], acc[m][r]);
       }
     }
   }
@@ -172,8 +195,11 @@ __global__ __launch_bounds__(kOpsThreads) void gemv_kernel(const uint16_t* __res
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
-      for (int r = 0; r < RW; ++r)
-        if (n0 + r < n) y[m * y_rs + n0 + r] = (uint16_t)(E::pack2(acc[m][r], 0.f) & 0xffffu);
+      for (int r = 0; r < OUT; ++r) {
+        if (n0 + r >= n) continue;
+        const float v = GLU ? silu_mul1<E>(acc[m][r], acc[m][r + OUT]) : acc[m][r];
+        y[m * y_rs + n0 + r] = (uint16_t)(E::pack2(v, 0.f) & 0xffffu);
+      }
   }
 }
 
@@ -194,6 +220,28 @@ int launch_gemv_m(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void
     hipLaunchKernelGGL((gemv_kernel<E, M, 1>), grid, dim3(kOpsThreads), 0, s, (const uint16_t*)x, x_rs,
                        (const uint16_t*)w, w_rs, (uint16_t*)y, y_rs, n, k);
   return (int)hipGetLastError();
+}
+
+// gate_up + silu_mul: two gate and two up rows per wave (4 weight rows in flight)
+template <class E, int M>
+int launch_gemv_glu_m(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int inter,
+                      int k, hipStream_t s) {
+  const int waves = (inter + 1) / 2;
+  const dim3 grid((waves + kOpsThreads / 64 - 1) / (kOpsThreads / 64));
+  hipLaunchKernelGGL((gemv_kernel<E, M, 4, true>), grid, dim3(kOpsThreads), 0, s, (const uint16_t*)x, x_rs,
+                     (const uint16_t*)w, w_rs, (uint16_t*)y, y_rs, inter, k);
+  return (int)hipGetLastError();
+}
+
+template <class E>
+int launch_gemv_glu_t(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int m,
+                      int inter, int k, hipStream_t s) {
+  switch (m) {
+    case 1: return launch_gemv_glu_m<E, 1>(x, x_rs, w, w_rs, y, y_rs, inter, k, s);
+    case 2: return launch_gemv_glu_m<E, 2>(x, x_rs, w, w_rs, y, y_rs, inter, k, s);
+    case 3: return launch_gemv_glu_m<E, 3>(x, x_rs, w, w_rs, y, y_rs, inter, k, s);
+    default: return launch_gemv_glu_m<E, 4>(x, x_rs, w, w_rs, y, y_rs, inter, k, s);
+  }
 }
 
 template <class E>
@@ -245,6 +293,12 @@ int launch_gemv(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* 
                 int32_t k, int32_t dtype, hipStream_t s) {
   return dtype == 2 ? launch_gemv_t<BF16>(x, x_rs, w, w_rs, y, y_rs, m, n, k, s)
                     : launch_gemv_t<F16>(x, x_rs, w, w_rs, y, y_rs, m, n, k, s);
+}
+
+int launch_gemv_silu_mul(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int32_t m,
+                         int32_t inter, int32_t k, int32_t dtype, hipStream_t s) {
+  return dtype == 2 ? launch_gemv_glu_t<BF16>(x, x_rs, w, w_rs, y, y_rs, m, inter, k, s)
+                    : launch_gemv_glu_t<F16>(x, x_rs, w, w_rs, y, y_rs, m, inter, k, s);
 }
 
 }  // namespace kvh

@@ -6,7 +6,8 @@ the shared paged pool through `backend.write_kv` / `backend.forward`, and the fo
 split at the attention calls into num_layers + 1 row-wise pieces (model.py:187-212).
 GEMMs, norms and RoPE are PyTorch (hipBLASLt GEMMs on ROCm); attention is the backend's. On
 the GPU with 16-bit weights (`fused_ops`), the residual add + RMSNorm and SiLU * up run as
-single libkvhip kernels and projections of at most 8 rows as its GEMV (engine/ops.py).
+single libkvhip kernels and projections of at most 4 rows as its GEMV, the gate_up one with
+SiLU * up in its epilogue (engine/ops.py).
 """
 
 from __future__ import annotations
@@ -217,7 +218,7 @@ class LlamaForCausalLM(nn.Module):
             prev = self.layers[i - 1]
             o = ops.linear(attn.flatten(1), prev.self_attn.o_proj.weight)
             x, h = ops.add_rmsnorm(x, o, prev.post_attention_layernorm.weight, prev.post_attention_layernorm.eps)
-            d = ops.linear(ops.silu_mul(ops.linear(h, prev.mlp.gate_up_proj.weight)), prev.mlp.down_proj.weight)
+            d = ops.linear(ops.mlp_act(h, prev.mlp.gate_up_proj.weight), prev.mlp.down_proj.weight)
             norm = self.norm if i == n else self.layers[i].input_layernorm
             x, h = ops.add_rmsnorm(x, d, norm.weight, norm.eps)
             if i == n:

@@ -1,6 +1,7 @@
-"""libkvhip's engine-harness kernels (kvh_add_rmsnorm, kvh_silu_mul, kvh_gemv) for
-fp16 / bf16 tensors on the GPU: the elementwise steps of a Llama layer in single passes and a
-weight-streaming GEMV for decode-sized batches. The model uses them on the GPU with 16-bit
+"""libkvhip's engine-harness kernels (kvh_add_rmsnorm, kvh_silu_mul, kvh_gemv,
+kvh_gemv_silu_mul) for fp16 / bf16 tensors on the GPU: the elementwise steps of a Llama layer
+in single passes and a weight-streaming GEMV for decode-sized batches (for the gate_up
+projection with SiLU * up in its epilogue). The model uses them on the GPU with 16-bit
 weights and keeps the PyTorch operations elsewhere (the CPU path the Hugging Face checks run).
 """
 
@@ -54,6 +55,21 @@ def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     if m == 0 or m > GEMV_MAX_ROWS or x.stride(-1) != 1 or not weight.is_contiguous():
         return torch.nn.functional.linear(x, weight)
     return gemv(x, weight)
+
+
+def mlp_act(x: torch.Tensor, gate_up_weight: torch.Tensor) -> torch.Tensor:
+    """silu_mul(linear(x, gate_up_weight)): for at most GEMV_MAX_ROWS rows one kvh_gemv_silu_mul
+    (the activation in the projection's epilogue, the same bits), else the two steps."""
+    m = x.shape[0]
+    if m == 0 or m > GEMV_MAX_ROWS or x.stride(-1) != 1 or not gate_up_weight.is_contiguous():
+        return silu_mul(torch.nn.functional.linear(x, gate_up_weight))
+    two_i, k = gate_up_weight.shape
+    y = torch.empty((m, two_i // 2), dtype=x.dtype, device=x.device)
+    st = _lib.load().kvh_gemv_silu_mul(x.data_ptr(), x.stride(0), gate_up_weight.data_ptr(), gate_up_weight.stride(0),
+                                       y.data_ptr(), y.stride(0), m, two_i // 2, k, _lib.KVH_DTYPE[x.dtype],
+                                       _stream(x))  # fmt: skip
+    _lib.check(st, "kvh_gemv_silu_mul")
+    return y
 
 
 def gemv(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:

@@ -1,9 +1,11 @@
-"""libkvhip's engine-harness kernels (kvh_add_rmsnorm, kvh_silu_mul, kvh_gemv) against the
+"""libkvhip's engine-harness kernels (kvh_add_rmsnorm, kvh_silu_mul, kvh_gemv,
+kvh_gemv_silu_mul) against the
 PyTorch operations they replace in the Llama layer (src/kvserve/model.py:22-32 and its MLP),
 in bf16 and fp16. The residual sum is bit-exact (one rounding, as PyTorch's add). The norm's
 fp32 statistics differ in summation order and rsqrt, and its output is rounded twice (x * r to
 the storage type, then times the weight), so it agrees to two units in the last place; SiLU
-(exp implementations differ) to one. The GEMV is checked against an fp32 product."""
+(exp implementations differ) to one. The GEMV is checked against an fp32 product, and the
+fused gate_up + SiLU * up GEMV bit for bit against the GEMV followed by kvh_silu_mul."""
 
 from __future__ import annotations
 
@@ -69,6 +71,29 @@ def test_gemv_against_fp32(hip_device, dtype, m, n, k):
     # fp32 accumulation in a different order, then one rounding to dtype
     tol = 2 * torch.finfo(dtype).eps * ref.abs() + 1e-3 * ref.abs().max()
     assert ((got.float() - ref).abs() <= tol).all()
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("inter,k", [(14336, 4096), (8192, 2048), (1003, 1032), (3, 8)])
+def test_gemv_silu_mul_is_gemv_then_silu_mul(hip_device, dtype, m, inter, k):
+    """The fused gate_up projection + silu_mul gives the bits of the two kernels in sequence
+    (the sums are rounded to dtype before the activation, as the projection's output is); odd
+    inter covers a wave whose second (gate, up) pair is past the end."""
+    g = torch.Generator(device=hip_device).manual_seed(m * inter + k)
+    x = torch.randn(m, k, generator=g, device=hip_device).to(dtype)
+    w = (torch.randn(2 * inter, k, generator=g, device=hip_device) * 0.08).to(dtype)
+    fused = ops.mlp_act(x, w)
+    assert fused.shape == (m, inter)
+    gu = ops.gemv(x, w)
+    pad = -(-inter // 8) * 8  # kvh_silu_mul takes inter % 8 == 0: halves placed in a padded row
+    gu_pad = torch.zeros(m, 2 * pad, dtype=dtype, device=hip_device)
+    gu_pad[:, :inter], gu_pad[:, pad : pad + inter] = gu[:, :inter], gu[:, inter:]
+    want = ops.silu_mul(gu_pad)[:, :inter]
+    assert torch.equal(fused.view(torch.int16), want.view(torch.int16))
+    if inter % 8 == 0:  # more rows: the two-step fallback (kvh_silu_mul takes inter % 8 == 0)
+        big = torch.randn(ops.GEMV_MAX_ROWS + 1, k, generator=g, device=hip_device).to(dtype)
+        assert torch.equal(ops.mlp_act(big, w), ops.silu_mul(F.linear(big, w)))
 
 
 def test_gemv_strided_rows_and_large_batches_fall_back(hip_device):
