@@ -195,6 +195,13 @@ KVH_API size_t kvh_paged_attention_workspace_size(int64_t num_tokens, int32_t nu
  * first ceil(seq_len / block_size) table entries of a row are read; ids outside
  * [0, num_blocks) are treated as empty pages. The call does not depend on max_seq_len.
  *
+ * Shared prefixes: for a decode-only batch (max_query_len * G <= 16) with
+ * max_blocks_per_seq * block_size > 8192, a small kernel first finds on the device the
+ * longest run of table columns that every decode sequence with >= 256 context tokens shares
+ * with the first one (prefix caching hands them the same physical blocks); those keys are
+ * then read once per group of 16 / (max_query_len * G) sequences instead of once per
+ * sequence. The result is the same attention; the workspace size covers it.
+ *
  * Replaces paged_attention(), src/kvserve/kernels/paged_attention.py:118-157, as called by
  * TritonAttention.forward, src/kvserve/attention.py:88-102.
  */
