@@ -44,6 +44,11 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return s;
 }
 
+// A thread keeps its first kKeep vectors (hd <= 8192) and their norm weights in registers
+// between the two passes, so the second pass starts without a memory round trip; wider rows
+// re-read the rest.
+constexpr int kKeep = 4;
+
 template <class E>
 __global__ __launch_bounds__(kOpsThreads) void add_rmsnorm_kernel(const uint16_t* __restrict__ x, int64_t x_ts,
                                                                   const uint16_t* __restrict__ d, int64_t d_ts,
@@ -56,9 +61,10 @@ __global__ __launch_bounds__(kOpsThreads) void add_rmsnorm_kernel(const uint16_t
   const int nv = hd / 8;
   const uint16_t* xr = x + t * x_ts;
   uint16_t* xor_ = xo + t * xo_ts;
+  float keep[kKeep][8];
+  u32x4 wkeep[kKeep];
   float ss = 0.f;
-  for (int v = threadIdx.x; v < nv; v += kOpsThreads) {
-    float a[8];
+  auto sum_in = [&](int v, float (&a)[8]) {
     unpack8<E>(*(const u32x4*)(xr + 8 * v), a);
     if (d) {
       float b[8];
@@ -70,20 +76,41 @@ __global__ __launch_bounds__(kOpsThreads) void add_rmsnorm_kernel(const uint16_t
       unpack8<E>(o, a);  // the rounded sum is what the norm sees
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss += a[i] * a[i];
+    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(a[i], a[i], ss);
+  };
+#pragma unroll
+  for (int j = 0; j < kKeep; ++j) {
+    const int v = threadIdx.x + kOpsThreads * j;
+    if (v < nv) {
+      wkeep[j] = *(const u32x4*)(w + 8 * v);
+      sum_in(v, keep[j]);
+    }
+  }
+  for (int v = threadIdx.x + kOpsThreads * kKeep; v < nv; v += kOpsThreads) {
+    float a[8];
+    sum_in(v, a);
   }
   const float r = rsqrtf(block_sum(ss, red) / (float)hd + eps);
-  const uint16_t* src = d ? xor_ : xr;
-  for (int v = threadIdx.x; v < nv; v += kOpsThreads) {
-    float a[8], g[8];
-    unpack8<E>(*(const u32x4*)(src + 8 * v), a);
-    unpack8<E>(*(const u32x4*)(w + 8 * v), g);
+  auto norm_out = [&](int v, float (&a)[8], const u32x4& wv) {
+    float g[8];
+    unpack8<E>(wv, g);
 #pragma unroll
     for (int i = 0; i < 8; ++i) a[i] *= r;
     unpack8<E>(pack8<E>(a), a);  // .to(dtype) before the weight
 #pragma unroll
     for (int i = 0; i < 8; ++i) a[i] *= g[i];
     *(u32x4*)(h + t * h_ts + 8 * v) = pack8<E>(a);
+  };
+#pragma unroll
+  for (int j = 0; j < kKeep; ++j) {
+    const int v = threadIdx.x + kOpsThreads * j;
+    if (v < nv) norm_out(v, keep[j], wkeep[j]);
+  }
+  const uint16_t* src = d ? xor_ : xr;
+  for (int v = threadIdx.x + kOpsThreads * kKeep; v < nv; v += kOpsThreads) {
+    float a[8];
+    unpack8<E>(*(const u32x4*)(src + 8 * v), a);
+    norm_out(v, a, *(const u32x4*)(w + 8 * v));
   }
 }
 
