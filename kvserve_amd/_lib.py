@@ -58,6 +58,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _f32, _vp,  # slots, sizes, dtype, scales, stream
         ],  # fmt: skip
     ),
+    "kvh_gemv_rope_and_cache": (
+        ctypes.c_int,
+        [
+            _vp, _i64, _vp, _i64, _i32, _i32,  # x, w_qkv, m, k
+            _vp, _vp, _vp, _i64,  # positions, cos/sin tables
+            _vp, _i64, _i64,  # q_out
+            _vp, _i64p, _vp, _i64p,  # caches
+            _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _f32, _vp,  # slots, sizes, dtype, fp8, scales
+        ],  # fmt: skip
+    ),
     "kvh_prepare_metadata": (
         ctypes.c_int,
         [

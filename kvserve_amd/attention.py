@@ -202,6 +202,55 @@ class HipAttention:
             _lib.check(st, "kvh_rope_and_cache")
         return out
 
+    # rows up to which gemv_rope_and_cache applies (the projection then streams its weight)
+    GEMV_ROPE_MAX_ROWS = 4
+
+    @staticmethod
+    def gemv_rope_and_cache(
+        x: torch.Tensor,
+        w_qkv: torch.Tensor,
+        positions: torch.Tensor,
+        cos: torch.Tensor,
+        sin: torch.Tensor,
+        k_cache: torch.Tensor,
+        v_cache: torch.Tensor,
+        slots: torch.Tensor,
+        num_heads: int,
+        out: torch.Tensor | None = None,
+        k_scale: float = 1.0,
+        v_scale: float = 1.0,
+    ) -> torch.Tensor:
+        """rope_and_cache(x @ w_qkv.T, ...) in one kernel (kvh_gemv_rope_and_cache) for at most
+        GEMV_ROPE_MAX_ROWS rows of 16-bit x: the same bits as the projection on kvh_gemv
+        followed by rope_and_cache. x: [T, hidden]; w_qkv: [(H + 2 Hkv) D, hidden], contiguous."""
+        _check_cache(k_cache, v_cache)
+        fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
+        num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
+        num_tokens, hidden = x.shape
+        _require(0 < num_tokens <= HipAttention.GEMV_ROPE_MAX_ROWS, "gemv_rope_and_cache takes 1 .. 4 rows")
+        _require(x.stride(-1) == 1 and w_qkv.is_contiguous(), "x needs a contiguous last dim, w_qkv contiguous")
+        _require(w_qkv.shape == ((num_heads + 2 * num_kv_heads) * head_dim, hidden), "w_qkv must be [(H + 2 Hkv) D, k]")
+        _require(cos.dtype == torch.float32 and sin.dtype == torch.float32, "cos/sin tables must be fp32")
+        _require(cos.dim() == 2 and cos.shape == sin.shape and cos.shape[1] == head_dim, "cos/sin must be [P, D]")
+        _require(cos.is_contiguous() and sin.is_contiguous(), "cos/sin tables must be contiguous")
+        _check_index(positions, "positions", 1)
+        _check_index(slots, "slot_mapping", 1)
+        _require(positions.shape[0] == num_tokens and slots.shape[0] == num_tokens, "one position and slot per token")
+        if out is None:
+            out = torch.empty((num_tokens, num_heads, head_dim), dtype=x.dtype, device=x.device)
+        _require(out.shape == (num_tokens, num_heads, head_dim) and out.stride(-1) == 1, "out must be [T, H, D]")
+        dtype = _dtype_code(x, w_qkv, out) if fp8 else _dtype_code(x, w_qkv, k_cache, v_cache, out)
+        st = _lib.load().kvh_gemv_rope_and_cache(
+            x.data_ptr(), x.stride(0), w_qkv.data_ptr(), w_qkv.stride(0), num_tokens, hidden,
+            positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+            out.data_ptr(), out.stride(0), out.stride(1),
+            k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(), _lib.i64x3(v_cache.stride()[:3]),
+            slots.data_ptr(), num_blocks, num_heads, num_kv_heads, head_dim, block_size, dtype, int(fp8),
+            float(k_scale), float(v_scale), _stream_handle(x.device),
+        )  # fmt: skip
+        _lib.check(st, "kvh_gemv_rope_and_cache")
+        return out
+
     @staticmethod
     def forward(
         q: torch.Tensor,

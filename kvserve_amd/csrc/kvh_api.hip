@@ -541,6 +541,37 @@ int kvh_gemv_silu_mul(const void* x, int64_t x_row_stride, const void* w_gate_up
                               (hipStream_t)stream);
 }
 
+int kvh_gemv_rope_and_cache(const void* x, int64_t x_row_stride, const void* w_qkv, int64_t w_row_stride,
+                            int32_t m, int32_t k, const int64_t* positions, const float* cos_table,
+                            const float* sin_table, int64_t max_positions, void* q_out, int64_t q_tok_stride,
+                            int64_t q_head_stride, void* k_cache, const int64_t k_cache_strides[3], void* v_cache,
+                            const int64_t v_cache_strides[3], const int64_t* slot_mapping, int64_t num_blocks,
+                            int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                            int32_t dtype, int32_t kv_fp8, float k_scale, float v_scale, void* stream) {
+  if (dtype != KVH_DTYPE_F16 && dtype != KVH_DTYPE_BF16) return KVH_E_DTYPE;
+  if (kv_fp8 && !(k_scale > 0.f && k_scale < INFINITY && v_scale > 0.f && v_scale < INFINITY)) return KVH_E_SHAPE;
+  if (m < 0 || k <= 0 || num_blocks < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      block_size <= 0 || max_positions <= 0)
+    return KVH_E_SHAPE;
+  if (m > 4 || k % 8 != 0 || head_dim % 2 != 0 || head_dim > 1024 || num_heads > 65535 || num_kv_heads > 65535)
+    return KVH_E_UNSUPPORTED;
+  if (m == 0) return KVH_OK;
+  if (!x || !w_qkv || !positions || !cos_table || !sin_table || !q_out || !k_cache || !v_cache || !k_cache_strides ||
+      !v_cache_strides || !slot_mapping)
+    return KVH_E_NULL;
+  const int64_t strides[] = {q_tok_stride, q_head_stride, k_cache_strides[0], k_cache_strides[1],
+                             k_cache_strides[2], v_cache_strides[0], v_cache_strides[1], v_cache_strides[2]};
+  for (int64_t st : strides)
+    if (st < 0) return KVH_E_SHAPE;
+  if (x_row_stride < k || w_row_stride < k) return KVH_E_SHAPE;
+  if (x_row_stride % 8 || w_row_stride % 8 || !a16(x) || !a16(w_qkv) || ((uintptr_t)q_out & 1u)) return KVH_E_ALIGN;
+  if (!kv_fp8 && (((uintptr_t)k_cache | (uintptr_t)v_cache) & 1u)) return KVH_E_ALIGN;
+  return launch_gemv_rope_and_cache(x, x_row_stride, w_qkv, w_row_stride, m, k, positions, cos_table, sin_table,
+                                    max_positions, q_out, q_tok_stride, q_head_stride, k_cache, k_cache_strides,
+                                    v_cache, v_cache_strides, slot_mapping, num_blocks, num_heads, num_kv_heads,
+                                    head_dim, block_size, dtype, kv_fp8 != 0, k_scale, v_scale, (hipStream_t)stream);
+}
+
 int kvh_profile_arm(void* const* events, int32_t num_events) {
   if (!events || num_events <= 0) {
     g_prof.num_events = 0;

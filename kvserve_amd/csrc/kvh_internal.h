@@ -144,6 +144,12 @@ int launch_rope_and_cache(const void* qkv, int64_t qkv_ts, const int64_t* positi
                           const int64_t* kcs, void* vc, const int64_t* vcs, const int64_t* slots, int64_t T,
                           int64_t num_blocks, int32_t H, int32_t Hkv, int32_t D, int32_t BS, int32_t dtype,
                           bool kv8, float k_scale, float v_scale, hipStream_t s);
+int launch_gemv_rope_and_cache(const void* x, int64_t x_rs, const void* w, int64_t w_rs, int32_t m, int32_t k,
+                               const int64_t* positions, const float* cos_t, const float* sin_t, int64_t max_pos,
+                               void* q_out, int64_t q_ts, int64_t q_hs, void* kc, const int64_t* kcs, void* vc,
+                               const int64_t* vcs, const int64_t* slots, int64_t num_blocks, int32_t H, int32_t Hkv,
+                               int32_t D, int32_t BS, int32_t dtype, bool kv8, float k_scale, float v_scale,
+                               hipStream_t s);
 int launch_reshape_and_cache_fp8(const void* k, int64_t k_ts, int64_t k_hs, const void* v, int64_t v_ts,
                                  int64_t v_hs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs,
                                  const int64_t* slots, int64_t T, int64_t num_blocks, int32_t Hkv, int32_t D,

@@ -17,6 +17,8 @@
 // half) pairs for the query and key heads, with the matching elements of the second half,
 // then 16-byte vectors of the value rows. Positions outside the tables are clamped; slots
 // outside the pool skip the cache writes (as reshape_and_cache does).
+#include <type_traits>
+
 #include "kvh_device.h"
 #include "kvh_internal.h"
 
@@ -172,6 +174,165 @@ int launch_rope_and_cache(const void* qkv, int64_t qkv_ts, const int64_t* positi
   }
 #undef KVH_LAUNCH_ROPE
   return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------
+// gemv_rope_and_cache: the QKV projection of m <= 4 decode rows (y = x W^T, W [(H + 2 Hkv) D,
+// k]) with rope_and_cache as its epilogue, in one launch. Wave w owns the pair of weight rows
+// (h D + d, h D + d + D / 2) of head h = w / (D / 2), d = w % (D / 2): the two elements
+// RoPE mixes. Each row's sum is taken exactly as gemv_kernel takes it (lane l walks
+// k = 8 l + 1024 i (+ 512), 8 explicit FMAs per vector, the rest in 512-steps, then a
+// butterfly), rounded to the storage type, and then goes through rope_and_cache_kernel's
+// arithmetic: the result has the bits of kvh_gemv followed by kvh_rope_and_cache(_fp8).
+struct GemvRopeArgs {
+  const uint16_t* x;
+  int64_t x_rs;
+  const uint16_t* w;
+  int64_t w_rs;
+  int k;
+  const int64_t* positions;
+  const float* cos_t;
+  const float* sin_t;
+  int64_t max_pos;
+  uint8_t* q_out;
+  int64_t q_ts, q_hs;
+  uint8_t* kc;
+  int64_t k_sb, k_ss, k_sh;
+  uint8_t* vc;
+  int64_t v_sb, v_ss, v_sh;
+  const int64_t* slots;
+  int64_t num_slots;
+  int H, Hkv, D, BS;
+  float k_scale, v_scale;
+};
+
+template <int DT, bool KV8>
+__device__ __forceinline__ void store_one(uint8_t* dst, float x, float scale) {
+  if constexpr (KV8) {
+    *dst = (uint8_t)(fp8_pack4(fp8_prep(x, scale), 0.f, 0.f, 0.f) & 0xffu);
+  } else {
+    const uint32_t b = DT == 2 ? BF16::pack2(x, 0.f) : F16::pack2(x, 0.f);
+    *(uint16_t*)dst = (uint16_t)(b & 0xffffu);
+  }
+}
+
+template <int DT, int M, bool KV8>
+__global__ __launch_bounds__(256) void gemv_rope_cache_kernel(GemvRopeArgs a) {
+  using R = RopeElem<DT>;
+  using E = std::conditional_t<DT == 2, BF16, F16>;
+  constexpr int CB = KV8 ? 1 : 2;  // bytes per cache element
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int half = a.D / 2;
+  const int nh = a.H + 2 * a.Hkv;
+  if (wave >= nh * half) return;
+  const int h = wave / half, d = wave % half;
+  const uint16_t* wr[2] = {a.w + ((int64_t)h * a.D + d) * a.w_rs, a.w + ((int64_t)h * a.D + d + half) * a.w_rs};
+  float acc[M][2];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.f;
+  auto fma8 = [&](const u32x4& xv, const u32x4& wv, float& c) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint16_t xb = (uint16_t)(xv[i / 2] >> (16 * (i & 1))), wb = (uint16_t)(wv[i / 2] >> (16 * (i & 1)));
+      c = __builtin_fmaf(E::to_f32(xb), E::to_f32(wb), c);
+    }
+  };
+  const int k = a.k, kfull = k / 1024 * 1024;
+  for (int k0 = 8 * lane; k0 < kfull; k0 += 1024) {
+    u32x4 wv[2][2], xv[2][M];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) wv[s2][r] = *(const u32x4*)(wr[r] + k0 + 512 * s2);
+#pragma unroll
+      for (int m = 0; m < M; ++m) xv[s2][m] = *(const u32x4*)(a.x + m * a.x_rs + k0 + 512 * s2);
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) fma8(xv[s2][m], wv[s2][r], acc[m][r]);
+  }
+  for (int k0 = kfull + 8 * lane; k0 < k; k0 += 512) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const u32x4 xv = *(const u32x4*)(a.x + m * a.x_rs + k0);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) fma8(xv, *(const u32x4*)(wr[r] + k0), acc[m][r]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      float v = acc[m][r];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+      acc[m][r] = v;
+    }
+  if (lane != 0) return;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const float lo = R::rnd(acc[m][0]), hi = R::rnd(acc[m][1]);  // the projection's output
+    const int64_t slot = a.slots[m];
+    const bool in_pool = slot >= 0 && slot < a.num_slots;
+    const int64_t blk = in_pool ? slot / a.BS : 0, off = in_pool ? slot % a.BS : 0;
+    if (h < a.H + a.Hkv) {
+      const int64_t pos = clamp64(a.positions[m], 0, a.max_pos - 1);
+      const float* cr = a.cos_t + pos * a.D;
+      const float* sr = a.sin_t + pos * a.D;
+      const float c_lo = R::rnd(cr[d]), c_hi = R::rnd(cr[d + half]);
+      const float s_lo = R::rnd(sr[d]), s_hi = R::rnd(sr[d + half]);
+      const float o_lo = R::add(R::mul(lo, c_lo), R::mul(-hi, s_lo));
+      const float o_hi = R::add(R::mul(hi, c_hi), R::mul(lo, s_hi));
+      if (h < a.H) {
+        uint8_t* dst = a.q_out + (m * a.q_ts + (int64_t)h * a.q_hs + d) * 2;
+        store_one<DT, false>(dst, o_lo, 1.f);
+        store_one<DT, false>(dst + half * 2, o_hi, 1.f);
+      } else if (in_pool) {
+        uint8_t* dst = a.kc + (blk * a.k_sb + off * a.k_ss + (int64_t)(h - a.H) * a.k_sh + d) * CB;
+        store_one<DT, KV8>(dst, o_lo, a.k_scale);
+        store_one<DT, KV8>(dst + half * CB, o_hi, a.k_scale);
+      }
+    } else if (in_pool) {
+      uint8_t* dst = a.vc + (blk * a.v_sb + off * a.v_ss + (int64_t)(h - a.H - a.Hkv) * a.v_sh + d) * CB;
+      store_one<DT, KV8>(dst, lo, a.v_scale);
+      store_one<DT, KV8>(dst + half * CB, hi, a.v_scale);
+    }
+  }
+}
+
+template <int DT, bool KV8>
+static int launch_gemv_rope_dt(const GemvRopeArgs& a, int m, hipStream_t s) {
+  const int waves = (a.H + 2 * a.Hkv) * (a.D / 2);
+  const dim3 grid((waves + 3) / 4);
+  switch (m) {
+    case 1: hipLaunchKernelGGL((gemv_rope_cache_kernel<DT, 1, KV8>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((gemv_rope_cache_kernel<DT, 2, KV8>), grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((gemv_rope_cache_kernel<DT, 3, KV8>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((gemv_rope_cache_kernel<DT, 4, KV8>), grid, dim3(256), 0, s, a); break;
+  }
+  return (int)hipGetLastError();
+}
+
+int launch_gemv_rope_and_cache(const void* x, int64_t x_rs, const void* w, int64_t w_rs, int32_t m, int32_t k,
+                               const int64_t* positions, const float* cos_t, const float* sin_t, int64_t max_pos,
+                               void* q_out, int64_t q_ts, int64_t q_hs, void* kc, const int64_t* kcs, void* vc,
+                               const int64_t* vcs, const int64_t* slots, int64_t num_blocks, int32_t H, int32_t Hkv,
+                               int32_t D, int32_t BS, int32_t dtype, bool kv8, float k_scale, float v_scale,
+                               hipStream_t s) {
+  GemvRopeArgs a{};
+  a.x = (const uint16_t*)x, a.x_rs = x_rs, a.w = (const uint16_t*)w, a.w_rs = w_rs, a.k = k;
+  a.positions = positions, a.cos_t = cos_t, a.sin_t = sin_t, a.max_pos = max_pos;
+  a.q_out = (uint8_t*)q_out, a.q_ts = q_ts, a.q_hs = q_hs;
+  a.kc = (uint8_t*)kc, a.k_sb = kcs[0], a.k_ss = kcs[1], a.k_sh = kcs[2];
+  a.vc = (uint8_t*)vc, a.v_sb = vcs[0], a.v_ss = vcs[1], a.v_sh = vcs[2];
+  a.slots = slots, a.num_slots = num_blocks * BS;
+  a.H = H, a.Hkv = Hkv, a.D = D, a.BS = BS, a.k_scale = k_scale, a.v_scale = v_scale;
+  if (dtype == 2) return kv8 ? launch_gemv_rope_dt<2, true>(a, m, s) : launch_gemv_rope_dt<2, false>(a, m, s);
+  return kv8 ? launch_gemv_rope_dt<1, true>(a, m, s) : launch_gemv_rope_dt<1, false>(a, m, s);
 }
 
 }  // namespace kvh

@@ -114,13 +114,19 @@ class Attention(nn.Module):
         return self.backend.forward(q, k_cache, v_cache, meta, self.scale, out=out, **sc)
 
     def attend_fused(self, qkv, positions, rope: RotaryEmbedding, kv_cache: torch.Tensor, meta: AttentionMetadata,
-                     out: torch.Tensor | None = None):  # fmt: skip
+                     out: torch.Tensor | None = None, h: torch.Tensor | None = None):  # fmt: skip
         """RoPE, QKV split and the cache write in the backend's one kernel, then attention: the
-        same result as project() + attend() (bit for bit) with the RoPE moved out of the piece."""
+        same result as project() + attend() (bit for bit) with the RoPE moved out of the piece.
+        With qkv None the piece stopped before the projection (h, decode-sized batches): the
+        backend's gemv_rope_and_cache projects and rotates in the same kernel."""
         k_cache, v_cache = kv_cache[0], kv_cache[1]
         sc = self._kv_scales(k_cache)
-        q = self.backend.rope_and_cache(qkv, positions, rope.cos, rope.sin, k_cache, v_cache, meta.slot_mapping,
-                                        self.num_heads, **sc)  # fmt: skip
+        if qkv is None:
+            q = self.backend.gemv_rope_and_cache(h, self.qkv_proj.weight, positions, rope.cos, rope.sin, k_cache,
+                                                 v_cache, meta.slot_mapping, self.num_heads, **sc)  # fmt: skip
+        else:
+            q = self.backend.rope_and_cache(qkv, positions, rope.cos, rope.sin, k_cache, v_cache, meta.slot_mapping,
+                                            self.num_heads, **sc)  # fmt: skip
         return self.backend.forward(q, k_cache, v_cache, meta, self.scale, out=out, **sc)
 
 
@@ -168,6 +174,9 @@ class LlamaForCausalLM(nn.Module):
         self.rope = RotaryEmbedding(cfg, max_positions)
         # a backend with a fused RoPE + cache-write kernel takes the raw QKV projection
         self.fused_rope = bool(getattr(backend, "fused_rope_cache", False))
+        self.backend = backend
+        # decode-sized batches: the QKV projection fused with RoPE + cache write (fused_ops only)
+        self._gemv_rope = hasattr(backend, "gemv_rope_and_cache")
         # libkvhip's fused elementwise kernels and GEMV (set on the GPU, 16-bit weights)
         self.fused_ops = False
 
@@ -178,7 +187,7 @@ class LlamaForCausalLM(nn.Module):
         x, q, k, v = self.piece(0, input_ids, positions, None, None)
         for i, layer in enumerate(self.layers):
             if self.fused_rope:
-                attn = layer.self_attn.attend_fused(q, positions, self.rope, kv_caches[i], meta)
+                attn = layer.self_attn.attend_fused(q, positions, self.rope, kv_caches[i], meta, h=k)
             else:
                 attn = layer.self_attn.attend(q, k, v, kv_caches[i], meta)
             x, q, k, v = self.piece(i + 1, input_ids, positions, x, attn)
@@ -224,6 +233,8 @@ class LlamaForCausalLM(nn.Module):
             if i == n:
                 return h, None, None, None
         layer = self.layers[i]
+        if self.fused_rope and self._gemv_rope and 0 < h.shape[0] <= self.backend.GEMV_ROPE_MAX_ROWS:
+            return x, None, h, None  # the projection runs in the attention step (gemv_rope_and_cache)
         qkv = ops.linear(h, layer.self_attn.qkv_proj.weight)
         if self.fused_rope:
             return x, qkv, None, None

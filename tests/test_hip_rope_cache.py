@@ -84,3 +84,38 @@ def test_argument_errors(hip_device):
         HipAttention.rope_and_cache(qkv, pos, rope.cos.half(), rope.sin.half(), kc, vc, slots, 8)
     with pytest.raises(ValueError):
         HipAttention.rope_and_cache(qkv, pos[:2], rope.cos, rope.sin, kc, vc, slots, 8)
+
+
+# -- the QKV projection fused with RoPE + cache write (kvh_gemv_rope_and_cache) ----------------
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("H,Hkv,D,k", [(32, 8, 128, 4096), (32, 8, 64, 2048), (8, 2, 64, 136)])
+@pytest.mark.parametrize("fp8", [False, True], ids=["cache16", "e4m3"])
+def test_gemv_rope_and_cache_is_gemv_then_rope_and_cache(hip_device, dtype, m, H, Hkv, D, k, fp8):
+    """The fused kernel gives the bits of the projection on kvh_gemv followed by
+    rope_and_cache: the same q, the same cache bytes (16-bit or E4M3 with scales), slots
+    outside the pool skipped; k = 136 runs the projection's tail loop."""
+    from kvserve_amd.engine import ops
+    from oracle import fp8 as fp8_oracle
+
+    g = torch.Generator(device=hip_device).manual_seed(m * D + k + fp8)
+    x = torch.randn(m, k, generator=g, device=hip_device).to(dtype)
+    w = (torch.randn((H + 2 * Hkv) * D, k, generator=g, device=hip_device) * 0.05).to(dtype)
+    rope = RotaryEmbedding(dataclasses.replace(LLAMA_3_2_1B, head_dim=D), 4096, device=hip_device)
+    pos = torch.randint(0, 4096, (m,), generator=g, device=hip_device)
+    NB, BS = 32, 16
+    slots = torch.randperm(NB * BS, generator=g, device=hip_device)[:m]
+    if m > 1:
+        slots[1] = NB * BS + 5  # outside the pool: no cache write
+    sc = dict(k_scale=0.5, v_scale=1.5) if fp8 else {}
+    kc = torch.randn(NB, BS, Hkv, D, generator=g, device=hip_device).to(dtype)
+    vc = torch.randn(NB, BS, Hkv, D, generator=g, device=hip_device).to(dtype)
+    if fp8:
+        kc, vc = fp8_oracle.quantize(kc, 1.0).to(hip_device), fp8_oracle.quantize(vc, 1.0).to(hip_device)
+    kc2, vc2 = kc.clone(), vc.clone()
+    got = HipAttention.gemv_rope_and_cache(x, w, pos, rope.cos, rope.sin, kc, vc, slots, H, **sc)
+    want = HipAttention.rope_and_cache(ops.gemv(x, w), pos, rope.cos, rope.sin, kc2, vc2, slots, H, **sc)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(kc.view(torch.uint8), kc2.view(torch.uint8))
+    assert torch.equal(vc.view(torch.uint8), vc2.view(torch.uint8))
