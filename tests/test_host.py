@@ -216,3 +216,60 @@ def test_ctypes_signatures_match_header():
         params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
         assert len(params) == len(args), (name, len(params), len(args))
     assert ctypes.sizeof(ctypes.c_size_t) == 8
+
+
+# -- argument checks of the fused engine GEMVs (they return before any HIP call) ------------------
+def _glu(lib, **over):
+    a = dict(x=0x1000, xs=4096, w=0x2000, ws=4096, y=0x3000, ys=14336, m=1, inter=14336, k=4096, dtype=2)
+    a.update(over)
+    return lib.kvh_gemv_silu_mul(a["x"], a["xs"], a["w"], a["ws"], a["y"], a["ys"], a["m"], a["inter"], a["k"],
+                                 a["dtype"], None)  # fmt: skip
+
+
+@pytest.mark.parametrize(
+    "over,status",
+    [
+        (dict(dtype=0), E_DTYPE),  # 16-bit only
+        (dict(m=5), E_UNSUPPORTED),
+        (dict(k=4095), E_UNSUPPORTED),
+        (dict(m=-1), E_SHAPE),
+        (dict(x=None), E_NULL),
+        (dict(ys=100), E_SHAPE),
+        (dict(x=0x1008), E_ALIGN),
+        (dict(m=0), 0),
+    ],
+)  # fmt: skip
+def test_gemv_silu_mul_validation(lib, over, status):
+    assert _glu(lib, **over) == status
+
+
+def _gr(lib, **over):
+    a = dict(x=0x1000, xs=2048, w=0x2000, ws=2048, m=1, k=2048, pos=0x3000, cos=0x4000, sin=0x5000, q=0x6000,
+             kc=0x7000, kcs=(16 * 512, 512, 64), vc=0x8000, vcs=(16 * 512, 512, 64), slots=0x9000, H=32, Hkv=8,
+             D=64, dtype=2, fp8=0, ks=1.0, vs=1.0)  # fmt: skip
+    a.update(over)
+    return lib.kvh_gemv_rope_and_cache(
+        a["x"], a["xs"], a["w"], a["ws"], a["m"], a["k"], a["pos"], a["cos"], a["sin"], 4096, a["q"], 32 * 64, 64,
+        a["kc"], _lib.i64x3(a["kcs"]), a["vc"], _lib.i64x3(a["vcs"]), a["slots"], 64, a["H"], a["Hkv"], a["D"], 16,
+        a["dtype"], a["fp8"], a["ks"], a["vs"], None,
+    )  # fmt: skip
+
+
+@pytest.mark.parametrize(
+    "over,status",
+    [
+        (dict(dtype=0), E_DTYPE),
+        (dict(fp8=1, ks=0.0), E_SHAPE),
+        (dict(m=5), E_UNSUPPORTED),
+        (dict(D=63), E_UNSUPPORTED),
+        (dict(k=100), E_UNSUPPORTED),
+        (dict(slots=None), E_NULL),
+        (dict(kcs=(16 * 512, 512, -64)), E_SHAPE),
+        (dict(xs=1024), E_SHAPE),
+        (dict(w=0x2004), E_ALIGN),
+        (dict(q=0x6001), E_ALIGN),
+        (dict(m=0), 0),
+    ],
+)  # fmt: skip
+def test_gemv_rope_and_cache_validation(lib, over, status):
+    assert _gr(lib, **over) == status
