@@ -41,7 +41,12 @@ class AttentionMetadata:
     q_valid: torch.Tensor | None = None
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_handle(device: torch.device) -> int:
+    if _RAW_STREAM is not None and device.index is not None:
+        return _RAW_STREAM(device.index)  # the current stream's handle without a Stream object
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -61,6 +66,37 @@ def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
     _require(k_cache.dim() == 4 and k_cache.shape == v_cache.shape, "caches must be [num_blocks, block_size, kv_heads, D]")
     _require(k_cache.stride(-1) == 1 and v_cache.stride(-1) == 1, "cache last dim must be contiguous")
     _require(k_cache.is_cuda and v_cache.is_cuda, "caches must be on a HIP device")
+
+
+# Per-call host work matters at decode sizes (tens of microseconds against kernels of the same
+# order), so what depends only on the cache tensors' layout is checked once per layout and
+# kept: (num_blocks, block_size, kv_heads, head_dim, k strides, v strides as ctypes arrays).
+_CACHE_LAYOUTS: dict = {}
+_WS_SIZES: dict = {}
+
+
+def _cache_layout(k_cache: torch.Tensor, v_cache: torch.Tensor) -> tuple:
+    ks, vs = k_cache.stride(), v_cache.stride()
+    key = (k_cache.data_ptr(), v_cache.data_ptr(), k_cache.get_device(), v_cache.get_device(), k_cache.dtype,
+           v_cache.dtype, k_cache.shape, v_cache.shape, ks, vs)  # fmt: skip
+    hit = _CACHE_LAYOUTS.get(key)
+    if hit is None:
+        _check_cache(k_cache, v_cache)
+        if len(_CACHE_LAYOUTS) > 256:
+            _CACHE_LAYOUTS.clear()
+        hit = (*k_cache.shape, _lib.i64x3(ks[:3]), _lib.i64x3(vs[:3]))
+        _CACHE_LAYOUTS[key] = hit
+    return hit
+
+
+def _workspace_size(lib, *shape) -> int:
+    n = _WS_SIZES.get(shape)
+    if n is None:
+        n = lib.kvh_paged_attention_workspace_size(*shape)
+        if len(_WS_SIZES) > 256:
+            _WS_SIZES.clear()
+        _WS_SIZES[shape] = n
+    return n
 
 
 # E4M3 KV caches (the *_fp8 entry points): float8_e4m3fn tensors with one scale per tensor.
@@ -115,9 +151,8 @@ class HipAttention:
         Slots outside the pool are skipped instead of raising. float8_e4m3fn caches store
         (x / scale).clamp(-448, 448).to(float8_e4m3fn) with the given scales, bit for bit.
         """
-        _check_cache(k_cache, v_cache)
+        num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs = _cache_layout(k_cache, v_cache)
         fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
-        num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
         _require(k.dim() == 3 and k.shape == v.shape, "k and v must be [T, kv_heads, head_dim]")
         _require(k.shape[1:] == (num_kv_heads, head_dim), f"k/v rows {tuple(k.shape[1:])} != cache rows")
         _require(k.stride(-1) == 1 and v.stride(-1) == 1, "k/v last dim must be contiguous")
@@ -128,16 +163,16 @@ class HipAttention:
             dtype = _dtype_code(k, v)
             st = lib.kvh_reshape_and_cache_fp8(
                 k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
-                k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(),
-                _lib.i64x3(v_cache.stride()[:3]), slots.data_ptr(), k.shape[0], num_blocks, num_kv_heads, head_dim,
-                block_size, dtype, float(k_scale), float(v_scale), _stream_handle(k_cache.device),
+                k_cache.data_ptr(), kcs, v_cache.data_ptr(), vcs, slots.data_ptr(), k.shape[0], num_blocks,
+                num_kv_heads, head_dim, block_size, dtype, float(k_scale), float(v_scale),
+                _stream_handle(k_cache.device),
             )  # fmt: skip
             _lib.check(st, "kvh_reshape_and_cache_fp8")
             return
         dtype = _dtype_code(k_cache, v_cache, k, v)
         st = lib.kvh_reshape_and_cache(
             k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
-            k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(), _lib.i64x3(v_cache.stride()[:3]),
+            k_cache.data_ptr(), kcs, v_cache.data_ptr(), vcs,
             slots.data_ptr(), k.shape[0], num_blocks, num_kv_heads, head_dim, block_size, dtype,
             _stream_handle(k_cache.device),
         )  # fmt: skip
@@ -169,9 +204,8 @@ class HipAttention:
         RoPE(q) as [T, num_heads, head_dim] (in `out` if given), bit-identical to the
         reference's bf16/fp16/fp32 torch operations.
         """
-        _check_cache(k_cache, v_cache)
+        num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs = _cache_layout(k_cache, v_cache)
         fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
-        num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
         _require(qkv.dim() == 2 and qkv.stride(-1) == 1, "qkv must be [T, (H + 2 Hkv) D] with a contiguous last dim")
         _require(qkv.shape[1] == (num_heads + 2 * num_kv_heads) * head_dim, "qkv width != (H + 2 Hkv) D")
         _require(cos.dtype == torch.float32 and sin.dtype == torch.float32, "cos/sin tables must be fp32")
@@ -190,7 +224,7 @@ class HipAttention:
         args = [
             qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
             out.data_ptr(), out.stride(0), out.stride(1),
-            k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(), _lib.i64x3(v_cache.stride()[:3]),
+            k_cache.data_ptr(), kcs, v_cache.data_ptr(), vcs,
             slots.data_ptr(), num_tokens, num_blocks, num_heads, num_kv_heads, head_dim, block_size, dtype,
         ]  # fmt: skip
         lib = _lib.load()
@@ -223,9 +257,8 @@ class HipAttention:
         """rope_and_cache(x @ w_qkv.T, ...) in one kernel (kvh_gemv_rope_and_cache) for at most
         GEMV_ROPE_MAX_ROWS rows of 16-bit x: the same bits as the projection on kvh_gemv
         followed by rope_and_cache. x: [T, hidden]; w_qkv: [(H + 2 Hkv) D, hidden], contiguous."""
-        _check_cache(k_cache, v_cache)
+        num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs = _cache_layout(k_cache, v_cache)
         fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
-        num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
         num_tokens, hidden = x.shape
         _require(0 < num_tokens <= HipAttention.GEMV_ROPE_MAX_ROWS, "gemv_rope_and_cache takes 1 .. 4 rows")
         _require(x.stride(-1) == 1 and w_qkv.is_contiguous(), "x needs a contiguous last dim, w_qkv contiguous")
@@ -244,7 +277,7 @@ class HipAttention:
             x.data_ptr(), x.stride(0), w_qkv.data_ptr(), w_qkv.stride(0), num_tokens, hidden,
             positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
             out.data_ptr(), out.stride(0), out.stride(1),
-            k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(), _lib.i64x3(v_cache.stride()[:3]),
+            k_cache.data_ptr(), kcs, v_cache.data_ptr(), vcs,
             slots.data_ptr(), num_blocks, num_heads, num_kv_heads, head_dim, block_size, dtype, int(fp8),
             float(k_scale), float(v_scale), _stream_handle(x.device),
         )  # fmt: skip
@@ -264,9 +297,8 @@ class HipAttention:
     ) -> torch.Tensor:
         """q: [T, H, D]; caches: [num_blocks, block_size, H_kv, D]. Returns [T, H, D] (in `out` if given).
         float8_e4m3fn caches hold keys / values as e4m3 * k_scale / v_scale (q and out bf16 or fp16)."""
-        _check_cache(k_cache, v_cache)
+        num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs = _cache_layout(k_cache, v_cache)
         fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
-        num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
         _require(q.dim() == 3 and q.shape[2] == head_dim, "q must be [T, H, head_dim]")
         _require(q.stride(-1) == 1, "q last dim must be contiguous")
         num_tokens, num_heads, _ = q.shape
@@ -287,13 +319,12 @@ class HipAttention:
         lib = _lib.load()
         width = tables.shape[1]
         max_q = int(meta.max_query_len)
-        ws_bytes = lib.kvh_paged_attention_workspace_size(
-            num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, width, block_size, max_q, dtype
-        )
+        ws_bytes = _workspace_size(lib, num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, width, block_size, max_q,
+                                   dtype)  # fmt: skip
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
         head = [
             q.data_ptr(), q.stride(0), q.stride(1),
-            k_cache.data_ptr(), _lib.i64x3(k_cache.stride()[:3]), v_cache.data_ptr(), _lib.i64x3(v_cache.stride()[:3]),
+            k_cache.data_ptr(), kcs, v_cache.data_ptr(), vcs,
             num_blocks,
             out.data_ptr(), out.stride(0), out.stride(1),
             tables.data_ptr(), tables.stride(0), width,
