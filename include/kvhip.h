@@ -284,6 +284,13 @@ KVH_API int kvh_gemv_rope_and_cache(const void* x, int64_t x_row_stride, const v
                                     int32_t block_size, int32_t dtype, int32_t kv_fp8, float k_scale,
                                     float v_scale, void* stream);
 
+/* gemm_skinny: y = x @ weight^T (nn.Linear, weight [n, k] row-major) for m <= 64 rows on the
+ * MFMA units, fp32 accumulation (8 k-slices summed in order), rounded to dtype; n % 16 == 0,
+ * k % 1024 == 0. For the decode-sized batches between kvh_gemv's 4 rows and a full GEMM. */
+KVH_API int kvh_gemm_skinny(const void* x, int64_t x_row_stride, const void* weight, int64_t w_row_stride,
+                            void* y, int64_t y_row_stride, int32_t m, int32_t n, int32_t k, int32_t dtype,
+                            void* stream);
+
 KVH_API int kvh_gemv_silu_mul(const void* x, int64_t x_row_stride, const void* w_gate_up, int64_t w_row_stride,
                               void* y, int64_t y_row_stride, int32_t m, int32_t inter, int32_t k, int32_t dtype,
                               void* stream);

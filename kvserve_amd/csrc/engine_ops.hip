@@ -286,6 +286,77 @@ int launch_gemv_t(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void
   }
 }
 
+// Skinny GEMM for 5 .. 64 rows: y[m][n] = sum_k x[m][k] w[n][k] on v_mfma_f32_16x16x32. A
+// workgroup of 8 waves owns 16 weight rows (one MFMA A tile, n0 .. n0 + 15); wave w takes the
+// k-slice [w K / 8, (w + 1) K / 8) in 32-wide steps, four in flight, with MT = ceil(m / 16)
+// B tiles of x (rows past m read row m - 1 and are dropped). The 8 partial 16 x 16 MT tiles
+// meet in LDS and are summed in wave order (deterministic) and rounded once. Lane l of a tile
+// holds D[4 (l / 16) + r][l % 16], r < 4: weight row n0 + 4 (l / 16) + r, x row 16 mt + l % 16.
+constexpr int kSkinnyWaves = 8;
+
+template <class E, int MT>
+__global__ __launch_bounds__(64 * kSkinnyWaves) void skinny_gemm_kernel(const uint16_t* __restrict__ x,
+                                                                        int64_t x_rs,
+                                                                        const uint16_t* __restrict__ w,
+                                                                        int64_t w_rs, uint16_t* __restrict__ y,
+                                                                        int64_t y_rs, int m, int k) {
+  __shared__ f32x4 red[kSkinnyWaves][MT][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = lane & 15, j = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int slice = k / kSkinnyWaves;
+  const int k_lo = wave * slice;
+  const uint16_t* wr = w + (n0 + i) * w_rs + k_lo + 8 * j;
+  const uint16_t* xr[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) xr[t] = x + (int64_t)min(16 * t + i, m - 1) * x_rs + k_lo + 8 * j;
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int kk = 0; kk < slice; kk += 128) {
+    u32x4 a[4], b[4][MT];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      a[u] = *(const u32x4*)(wr + kk + 32 * u);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) b[u][t] = *(const u32x4*)(xr[t] + kk + 32 * u);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[t] = E::mfma(a[u], b[u][t], acc[t]);
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
+  __syncthreads();
+  // 16 x 16 MT outputs; thread q sums element q % 4 of lane (q / 4) % 64 of tile q / 256
+  for (int q = threadIdx.x; q < MT * 256; q += 64 * kSkinnyWaves) {
+    const int t = q >> 8, l = (q >> 2) & 63, r = q & 3;
+    const int row = 16 * t + (l & 15);
+    if (row >= m) continue;
+    float sum = 0.f;
+#pragma unroll
+    for (int v = 0; v < kSkinnyWaves; ++v) sum += red[v][t][l][r];
+    y[row * y_rs + n0 + 4 * (l >> 4) + r] = (uint16_t)(E::pack2(sum, 0.f) & 0xffffu);
+  }
+}
+
+template <class E>
+int launch_skinny_t(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int m, int n,
+                    int k, hipStream_t s) {
+  const dim3 grid((unsigned)(n / 16)), block(64 * kSkinnyWaves);
+  const auto* xp = (const uint16_t*)x;
+  const auto* wp = (const uint16_t*)w;
+  auto* yp = (uint16_t*)y;
+  switch ((m + 15) / 16) {
+    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<E, 1>), grid, block, 0, s, xp, x_rs, wp, w_rs, yp, y_rs, m, k); break;
+    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<E, 2>), grid, block, 0, s, xp, x_rs, wp, w_rs, yp, y_rs, m, k); break;
+    case 3: hipLaunchKernelGGL((skinny_gemm_kernel<E, 3>), grid, block, 0, s, xp, x_rs, wp, w_rs, yp, y_rs, m, k); break;
+    default: hipLaunchKernelGGL((skinny_gemm_kernel<E, 4>), grid, block, 0, s, xp, x_rs, wp, w_rs, yp, y_rs, m, k); break;
+  }
+  return (int)hipGetLastError();
+}
+
 }  // namespace
 
 int launch_add_rmsnorm(const void* x, int64_t x_ts, const void* d, int64_t d_ts, const void* w, void* xo,
@@ -326,6 +397,12 @@ int launch_gemv_silu_mul(const void* x, int64_t x_rs, const void* w, int64_t w_r
                          int32_t inter, int32_t k, int32_t dtype, hipStream_t s) {
   return dtype == 2 ? launch_gemv_glu_t<BF16>(x, x_rs, w, w_rs, y, y_rs, m, inter, k, s)
                     : launch_gemv_glu_t<F16>(x, x_rs, w, w_rs, y, y_rs, m, inter, k, s);
+}
+
+int launch_gemm_skinny(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int32_t m,
+                       int32_t n, int32_t k, int32_t dtype, hipStream_t s) {
+  return dtype == 2 ? launch_skinny_t<BF16>(x, x_rs, w, w_rs, y, y_rs, m, n, k, s)
+                    : launch_skinny_t<F16>(x, x_rs, w, w_rs, y, y_rs, m, n, k, s);
 }
 
 }  // namespace kvh

@@ -572,6 +572,19 @@ int kvh_gemv_rope_and_cache(const void* x, int64_t x_row_stride, const void* w_q
                                     head_dim, block_size, dtype, kv_fp8 != 0, k_scale, v_scale, (hipStream_t)stream);
 }
 
+int kvh_gemm_skinny(const void* x, int64_t x_row_stride, const void* weight, int64_t w_row_stride, void* y,
+                    int64_t y_row_stride, int32_t m, int32_t n, int32_t k, int32_t dtype, void* stream) {
+  if (dtype != KVH_DTYPE_F16 && dtype != KVH_DTYPE_BF16) return KVH_E_DTYPE;
+  if (m < 0 || n < 0 || k <= 0) return KVH_E_SHAPE;
+  if (m > 64 || n % 16 != 0 || k % 1024 != 0) return KVH_E_UNSUPPORTED;
+  if (m == 0 || n == 0) return KVH_OK;
+  if (!x || !weight || !y) return KVH_E_NULL;
+  if (x_row_stride < k || w_row_stride < k || y_row_stride < n) return KVH_E_SHAPE;
+  if (x_row_stride % 8 || w_row_stride % 8 || !a16(x) || !a16(weight) || ((uintptr_t)y & 1u)) return KVH_E_ALIGN;
+  return launch_gemm_skinny(x, x_row_stride, weight, w_row_stride, y, y_row_stride, m, n, k, dtype,
+                            (hipStream_t)stream);
+}
+
 int kvh_profile_arm(void* const* events, int32_t num_events) {
   if (!events || num_events <= 0) {
     g_prof.num_events = 0;

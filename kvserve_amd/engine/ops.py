@@ -49,12 +49,43 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def skinny_wins(m: int, n: int, k: int) -> bool:
+    """Where kvh_gemm_skinny beats hipBLASLt inside the decode graph (measured on MI355X at the
+    1B / 8B shapes; the skinny kernel re-reads x per 16 weight rows, so its edge shrinks with m
+    and the weight size): up to 8 rows for weights up to 80 MB (8B o_proj 9.7 vs 19.3 us
+    alone; decode at batch 8: 8B +3%, 1B +7%), up to 32 rows for weights up to 13 MB (the 1B
+    QKV and o_proj; 1B at batch 32 +4%). Larger weights at 16 rows, everything at 64 rows and
+    the 8B o_proj at 32 won alone but not inside the model."""
+    if n % 16 or k % 1024:
+        return False
+    w_bytes = 2 * n * k
+    if m <= 8:
+        return w_bytes <= 80e6
+    return m <= 32 and w_bytes <= 13e6
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-    """x @ weight.T: kvh_gemv for at most GEMV_MAX_ROWS rows, else PyTorch (hipBLASLt)."""
+    """x @ weight.T: kvh_gemv for at most GEMV_MAX_ROWS rows, kvh_gemm_skinny where it beats
+    hipBLASLt (skinny_wins), else PyTorch (hipBLASLt)."""
     m = x.shape[0]
-    if m == 0 or m > GEMV_MAX_ROWS or x.stride(-1) != 1 or not weight.is_contiguous():
+    if m == 0 or x.stride(-1) != 1 or not weight.is_contiguous():
         return torch.nn.functional.linear(x, weight)
-    return gemv(x, weight)
+    if m <= GEMV_MAX_ROWS:
+        return gemv(x, weight)
+    if skinny_wins(m, *weight.shape):
+        return gemm_skinny(x, weight)
+    return torch.nn.functional.linear(x, weight)
+
+
+def gemm_skinny(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """x @ weight.T on kvh_gemm_skinny (x: at most 64 rows; n % 16 == 0, k % 1024 == 0)."""
+    m = x.shape[0]
+    n, k = weight.shape
+    y = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    st = _lib.load().kvh_gemm_skinny(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), y.data_ptr(),
+                                     y.stride(0), m, n, k, _lib.KVH_DTYPE[x.dtype], _stream(x))  # fmt: skip
+    _lib.check(st, "kvh_gemm_skinny")
+    return y
 
 
 def mlp_act(x: torch.Tensor, gate_up_weight: torch.Tensor) -> torch.Tensor:
@@ -62,7 +93,7 @@ def mlp_act(x: torch.Tensor, gate_up_weight: torch.Tensor) -> torch.Tensor:
     (the activation in the projection's epilogue, the same bits), else the two steps."""
     m = x.shape[0]
     if m == 0 or m > GEMV_MAX_ROWS or x.stride(-1) != 1 or not gate_up_weight.is_contiguous():
-        return silu_mul(torch.nn.functional.linear(x, gate_up_weight))
+        return silu_mul(linear(x, gate_up_weight))
     two_i, k = gate_up_weight.shape
     y = torch.empty((m, two_i // 2), dtype=x.dtype, device=x.device)
     st = _lib.load().kvh_gemv_silu_mul(x.data_ptr(), x.stride(0), gate_up_weight.data_ptr(), gate_up_weight.stride(0),

@@ -93,7 +93,23 @@ def test_gemv_silu_mul_is_gemv_then_silu_mul(hip_device, dtype, m, inter, k):
     assert torch.equal(fused.view(torch.int16), want.view(torch.int16))
     if inter % 8 == 0:  # more rows: the two-step fallback (kvh_silu_mul takes inter % 8 == 0)
         big = torch.randn(ops.GEMV_MAX_ROWS + 1, k, generator=g, device=hip_device).to(dtype)
-        assert torch.equal(ops.mlp_act(big, w), ops.silu_mul(F.linear(big, w)))
+        assert torch.equal(ops.mlp_act(big, w), ops.silu_mul(ops.linear(big, w)))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("m", [5, 16, 17, 33, 64])
+@pytest.mark.parametrize("n,k", [(6144, 4096), (2048, 8192), (16, 1024)])
+def test_gemm_skinny_against_fp32(hip_device, dtype, m, n, k):
+    """The skinny MFMA GEMM (5 .. 64 rows; partial row tiles of 16) against an fp32 product,
+    the same bar as the GEMV, and deterministic across calls."""
+    g = torch.Generator(device=hip_device).manual_seed(m * n + k)
+    x = torch.randn(m, k, generator=g, device=hip_device).to(dtype)
+    w = (torch.randn(n, k, generator=g, device=hip_device) * 0.05).to(dtype)
+    got = ops.gemm_skinny(x, w)
+    ref = x.float() @ w.float().t()
+    tol = 2 * torch.finfo(dtype).eps * ref.abs() + 1e-3 * ref.abs().max()
+    assert ((got.float() - ref).abs() <= tol).all()
+    assert torch.equal(got.view(torch.int16), ops.gemm_skinny(x, w).view(torch.int16))
 
 
 def test_gemv_strided_rows_and_large_batches_fall_back(hip_device):
@@ -101,7 +117,7 @@ def test_gemv_strided_rows_and_large_batches_fall_back(hip_device):
     w = torch.randn(512, 4096, device=hip_device).to(torch.bfloat16)
     ref = x.float() @ w.float().t()
     assert (ops.linear(x, w).float() - ref).abs().max() <= 0.05 * ref.abs().max()
-    big = torch.randn(ops.GEMV_MAX_ROWS + 1, 4096, device=hip_device).to(torch.bfloat16)
+    big = torch.randn(65, 4096, device=hip_device).to(torch.bfloat16)  # past the skinny GEMM: hipBLASLt
     assert torch.equal(ops.linear(big, w), F.linear(big, w))
 
 

@@ -273,3 +273,27 @@ def _gr(lib, **over):
 )  # fmt: skip
 def test_gemv_rope_and_cache_validation(lib, over, status):
     assert _gr(lib, **over) == status
+
+
+def _sk(lib, **over):
+    a = dict(x=0x1000, xs=4096, w=0x2000, ws=4096, y=0x3000, ys=6144, m=8, n=6144, k=4096, dtype=2)
+    a.update(over)
+    return lib.kvh_gemm_skinny(a["x"], a["xs"], a["w"], a["ws"], a["y"], a["ys"], a["m"], a["n"], a["k"], a["dtype"],
+                               None)  # fmt: skip
+
+
+@pytest.mark.parametrize(
+    "over,status",
+    [
+        (dict(dtype=0), E_DTYPE),
+        (dict(m=65), E_UNSUPPORTED),
+        (dict(n=6150), E_UNSUPPORTED),
+        (dict(k=4000), E_UNSUPPORTED),
+        (dict(w=None), E_NULL),
+        (dict(xs=1024), E_SHAPE),
+        (dict(x=0x1004), E_ALIGN),
+        (dict(m=0), 0),
+    ],
+)  # fmt: skip
+def test_gemm_skinny_validation(lib, over, status):
+    assert _sk(lib, **over) == status
