@@ -291,6 +291,13 @@ KVH_API int kvh_gemm_skinny(const void* x, int64_t x_row_stride, const void* wei
                             void* y, int64_t y_row_stride, int32_t m, int32_t n, int32_t k, int32_t dtype,
                             void* stream);
 
+/* gemm_skinny_silu_mul: kvh_gemm_skinny of the fused gate_up projection (w_gate_up [2 inter, k])
+ * followed by kvh_silu_mul in one launch, with the same bits; m <= 64, inter % 8 == 0,
+ * k % 1024 == 0. */
+KVH_API int kvh_gemm_skinny_silu_mul(const void* x, int64_t x_row_stride, const void* w_gate_up,
+                                     int64_t w_row_stride, void* y, int64_t y_row_stride, int32_t m, int32_t inter,
+                                     int32_t k, int32_t dtype, void* stream);
+
 KVH_API int kvh_gemv_silu_mul(const void* x, int64_t x_row_stride, const void* w_gate_up, int64_t w_row_stride,
                               void* y, int64_t y_row_stride, int32_t m, int32_t inter, int32_t k, int32_t dtype,
                               void* stream);

@@ -110,6 +110,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kvh_silu_mul": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp]),
     "kvh_gemv": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "kvh_gemm_skinny": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
+    "kvh_gemm_skinny_silu_mul": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "kvh_gemv_silu_mul": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "kvh_profile_arm": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), _i32]),
     "kvh_last_launch_kernels": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int32), _i32]),

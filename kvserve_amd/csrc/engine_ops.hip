@@ -292,21 +292,26 @@ int launch_gemv_t(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void
 // B tiles of x (rows past m read row m - 1 and are dropped). The 8 partial 16 x 16 MT tiles
 // meet in LDS and are summed in wave order (deterministic) and rounded once. Lane l of a tile
 // holds D[4 (l / 16) + r][l % 16], r < 4: weight row n0 + 4 (l / 16) + r, x row 16 mt + l % 16.
+// GLU: the workgroup owns output columns c0 .. c0 + 7 (c0 = 8 blockIdx) of silu_mul(gate_up):
+// A rows i < 8 are gate rows c0 + i, rows i >= 8 the up rows inter + c0 + i - 8; the epilogue
+// rounds each sum to the storage type and applies silu_mul's arithmetic (the bits of the plain
+// kernel followed by kvh_silu_mul). n is then the intermediate size.
 constexpr int kSkinnyWaves = 8;
 
-template <class E, int MT>
+template <class E, int MT, bool GLU = false>
 __global__ __launch_bounds__(64 * kSkinnyWaves) void skinny_gemm_kernel(const uint16_t* __restrict__ x,
                                                                         int64_t x_rs,
                                                                         const uint16_t* __restrict__ w,
                                                                         int64_t w_rs, uint16_t* __restrict__ y,
-                                                                        int64_t y_rs, int m, int k) {
+                                                                        int64_t y_rs, int m, int k, int n) {
   __shared__ f32x4 red[kSkinnyWaves][MT][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i = lane & 15, j = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t n0 = (int64_t)blockIdx.x * (GLU ? 8 : 16);
   const int slice = k / kSkinnyWaves;
   const int k_lo = wave * slice;
-  const uint16_t* wr = w + (n0 + i) * w_rs + k_lo + 8 * j;
+  const int64_t wrow = GLU ? (i < 8 ? n0 + i : n + n0 + i - 8) : n0 + i;
+  const uint16_t* wr = w + wrow * w_rs + k_lo + 8 * j;
   const uint16_t* xr[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) xr[t] = x + (int64_t)min(16 * t + i, m - 1) * x_rs + k_lo + 8 * j;
@@ -329,30 +334,48 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void skinny_gemm_kernel(const ui
 #pragma unroll
   for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
   __syncthreads();
-  // 16 x 16 MT outputs; thread q sums element q % 4 of lane (q / 4) % 64 of tile q / 256
-  for (int q = threadIdx.x; q < MT * 256; q += 64 * kSkinnyWaves) {
-    const int t = q >> 8, l = (q >> 2) & 63, r = q & 3;
-    const int row = 16 * t + (l & 15);
-    if (row >= m) continue;
-    float sum = 0.f;
+  if constexpr (GLU) {
+    // 8 x 16 MT outputs; thread q: column c = q % 8 of x row 16 t + (q / 8) % 16, t = q / 128;
+    // the gate sum is D[c][.] (lane 16 (c / 4) + row, element c % 4), the up sum D[8 + c][.]
+    for (int q = threadIdx.x; q < MT * 128; q += 64 * kSkinnyWaves) {
+      const int t = q >> 7, mr = (q >> 3) & 15, c = q & 7;
+      const int row = 16 * t + mr;
+      if (row >= m) continue;
+      const int lg = 16 * (c >> 2) + mr, lu = 16 * (2 + (c >> 2)) + mr, r = c & 3;
+      float g = 0.f, u = 0.f;
 #pragma unroll
-    for (int v = 0; v < kSkinnyWaves; ++v) sum += red[v][t][l][r];
-    y[row * y_rs + n0 + 4 * (l >> 4) + r] = (uint16_t)(E::pack2(sum, 0.f) & 0xffffu);
+      for (int v = 0; v < kSkinnyWaves; ++v) {
+        g += red[v][t][lg][r];
+        u += red[v][t][lu][r];
+      }
+      y[row * y_rs + n0 + c] = (uint16_t)(E::pack2(silu_mul1<E>(g, u), 0.f) & 0xffffu);
+    }
+  } else {
+    // 16 x 16 MT outputs; thread q sums element q % 4 of lane (q / 4) % 64 of tile q / 256
+    for (int q = threadIdx.x; q < MT * 256; q += 64 * kSkinnyWaves) {
+      const int t = q >> 8, l = (q >> 2) & 63, r = q & 3;
+      const int row = 16 * t + (l & 15);
+      if (row >= m) continue;
+      float sum = 0.f;
+#pragma unroll
+      for (int v = 0; v < kSkinnyWaves; ++v) sum += red[v][t][l][r];
+      y[row * y_rs + n0 + 4 * (l >> 4) + r] = (uint16_t)(E::pack2(sum, 0.f) & 0xffffu);
+    }
   }
 }
 
-template <class E>
+template <class E, bool GLU>
 int launch_skinny_t(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int m, int n,
                     int k, hipStream_t s) {
-  const dim3 grid((unsigned)(n / 16)), block(64 * kSkinnyWaves);
+  const dim3 grid((unsigned)(n / (GLU ? 8 : 16))), block(64 * kSkinnyWaves);
   const auto* xp = (const uint16_t*)x;
   const auto* wp = (const uint16_t*)w;
   auto* yp = (uint16_t*)y;
   switch ((m + 15) / 16) {
-    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<E, 1>), grid, block, 0, s, xp, x_rs, wp, w_rs, yp, y_rs, m, k); break;
-    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<E, 2>), grid, block, 0, s, xp, x_rs, wp, w_rs, yp, y_rs, m, k); break;
-    case 3: hipLaunchKernelGGL((skinny_gemm_kernel<E, 3>), grid, block, 0, s, xp, x_rs, wp, w_rs, yp, y_rs, m, k); break;
-    default: hipLaunchKernelGGL((skinny_gemm_kernel<E, 4>), grid, block, 0, s, xp, x_rs, wp, w_rs, yp, y_rs, m, k); break;
+    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<E, 1, GLU>), grid, block, 0, s, xp, x_rs, wp, w_rs, yp, y_rs, m, k, n); break;
+    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<E, 2, GLU>), grid, block, 0, s, xp, x_rs, wp, w_rs, yp, y_rs, m, k, n); break;
+    case 3: hipLaunchKernelGGL((skinny_gemm_kernel<E, 3, GLU>), grid, block, 0, s, xp, x_rs, wp, w_rs, yp, y_rs, m, k, n); break;
+    default: hipLaunchKernelGGL((skinny_gemm_kernel<E, 4, GLU>), grid, block, 0, s, xp, x_rs, wp, w_rs, yp, y_rs, m, k, n); break;
   }
   return (int)hipGetLastError();
 }
@@ -400,9 +423,12 @@ int launch_gemv_silu_mul(const void* x, int64_t x_rs, const void* w, int64_t w_r
 }
 
 int launch_gemm_skinny(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int32_t m,
-                       int32_t n, int32_t k, int32_t dtype, hipStream_t s) {
-  return dtype == 2 ? launch_skinny_t<BF16>(x, x_rs, w, w_rs, y, y_rs, m, n, k, s)
-                    : launch_skinny_t<F16>(x, x_rs, w, w_rs, y, y_rs, m, n, k, s);
+                       int32_t n, int32_t k, bool glu, int32_t dtype, hipStream_t s) {
+  if (glu)
+    return dtype == 2 ? launch_skinny_t<BF16, true>(x, x_rs, w, w_rs, y, y_rs, m, n, k, s)
+                      : launch_skinny_t<F16, true>(x, x_rs, w, w_rs, y, y_rs, m, n, k, s);
+  return dtype == 2 ? launch_skinny_t<BF16, false>(x, x_rs, w, w_rs, y, y_rs, m, n, k, s)
+                    : launch_skinny_t<F16, false>(x, x_rs, w, w_rs, y, y_rs, m, n, k, s);
 }
 
 }  // namespace kvh

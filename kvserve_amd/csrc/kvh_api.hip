@@ -581,7 +581,21 @@ int kvh_gemm_skinny(const void* x, int64_t x_row_stride, const void* weight, int
   if (!x || !weight || !y) return KVH_E_NULL;
   if (x_row_stride < k || w_row_stride < k || y_row_stride < n) return KVH_E_SHAPE;
   if (x_row_stride % 8 || w_row_stride % 8 || !a16(x) || !a16(weight) || ((uintptr_t)y & 1u)) return KVH_E_ALIGN;
-  return launch_gemm_skinny(x, x_row_stride, weight, w_row_stride, y, y_row_stride, m, n, k, dtype,
+  return launch_gemm_skinny(x, x_row_stride, weight, w_row_stride, y, y_row_stride, m, n, k, false, dtype,
+                            (hipStream_t)stream);
+}
+
+int kvh_gemm_skinny_silu_mul(const void* x, int64_t x_row_stride, const void* w_gate_up, int64_t w_row_stride,
+                             void* y, int64_t y_row_stride, int32_t m, int32_t inter, int32_t k, int32_t dtype,
+                             void* stream) {
+  if (dtype != KVH_DTYPE_F16 && dtype != KVH_DTYPE_BF16) return KVH_E_DTYPE;
+  if (m < 0 || inter < 0 || k <= 0) return KVH_E_SHAPE;
+  if (m > 64 || inter % 8 != 0 || k % 1024 != 0) return KVH_E_UNSUPPORTED;
+  if (m == 0 || inter == 0) return KVH_OK;
+  if (!x || !w_gate_up || !y) return KVH_E_NULL;
+  if (x_row_stride < k || w_row_stride < k || y_row_stride < inter) return KVH_E_SHAPE;
+  if (x_row_stride % 8 || w_row_stride % 8 || !a16(x) || !a16(w_gate_up) || ((uintptr_t)y & 1u)) return KVH_E_ALIGN;
+  return launch_gemm_skinny(x, x_row_stride, w_gate_up, w_row_stride, y, y_row_stride, m, inter, k, true, dtype,
                             (hipStream_t)stream);
 }
 

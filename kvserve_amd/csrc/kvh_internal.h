@@ -137,7 +137,7 @@ int launch_silu_mul(const void* gu, int64_t gu_ts, void* out, int64_t o_ts, int6
 int launch_gemv(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int32_t m, int32_t n,
                 int32_t k, int32_t dtype, hipStream_t s);
 int launch_gemm_skinny(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int32_t m,
-                       int32_t n, int32_t k, int32_t dtype, hipStream_t s);
+                       int32_t n, int32_t k, bool glu, int32_t dtype, hipStream_t s);
 int launch_gemv_silu_mul(const void* x, int64_t x_rs, const void* w, int64_t w_rs, void* y, int64_t y_rs, int32_t m,
                          int32_t inter, int32_t k, int32_t dtype, hipStream_t s);
 

@@ -92,8 +92,18 @@ def mlp_act(x: torch.Tensor, gate_up_weight: torch.Tensor) -> torch.Tensor:
     """silu_mul(linear(x, gate_up_weight)): for at most GEMV_MAX_ROWS rows one kvh_gemv_silu_mul
     (the activation in the projection's epilogue, the same bits), else the two steps."""
     m = x.shape[0]
-    if m == 0 or m > GEMV_MAX_ROWS or x.stride(-1) != 1 or not gate_up_weight.is_contiguous():
+    if m == 0 or x.stride(-1) != 1 or not gate_up_weight.is_contiguous():
         return silu_mul(linear(x, gate_up_weight))
+    if m > GEMV_MAX_ROWS:
+        two_i, k = gate_up_weight.shape
+        if two_i % 16 or not skinny_wins(m, two_i, k):
+            return silu_mul(linear(x, gate_up_weight))
+        y = torch.empty((m, two_i // 2), dtype=x.dtype, device=x.device)
+        st = _lib.load().kvh_gemm_skinny_silu_mul(x.data_ptr(), x.stride(0), gate_up_weight.data_ptr(),
+                                                  gate_up_weight.stride(0), y.data_ptr(), y.stride(0), m, two_i // 2, k,
+                                                  _lib.KVH_DTYPE[x.dtype], _stream(x))  # fmt: skip
+        _lib.check(st, "kvh_gemm_skinny_silu_mul")
+        return y
     two_i, k = gate_up_weight.shape
     y = torch.empty((m, two_i // 2), dtype=x.dtype, device=x.device)
     st = _lib.load().kvh_gemv_silu_mul(x.data_ptr(), x.stride(0), gate_up_weight.data_ptr(), gate_up_weight.stride(0),

@@ -112,6 +112,26 @@ def test_gemm_skinny_against_fp32(hip_device, dtype, m, n, k):
     assert torch.equal(got.view(torch.int16), ops.gemm_skinny(x, w).view(torch.int16))
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("m", [5, 8, 17, 64])
+@pytest.mark.parametrize("inter,k", [(8192, 2048), (16, 1024)])
+def test_gemm_skinny_silu_mul_is_skinny_then_silu_mul(hip_device, dtype, m, inter, k):
+    """kvh_gemm_skinny_silu_mul (8 gate + 8 up rows per workgroup, silu_mul in the epilogue)
+    gives the bits of kvh_gemm_skinny followed by kvh_silu_mul."""
+    from kvserve_amd import _lib
+
+    g = torch.Generator(device=hip_device).manual_seed(m * inter + k)
+    x = torch.randn(m, k, generator=g, device=hip_device).to(dtype)
+    w = (torch.randn(2 * inter, k, generator=g, device=hip_device) * 0.05).to(dtype)
+    y = torch.empty(m, inter, dtype=dtype, device=hip_device)
+    st = _lib.load().kvh_gemm_skinny_silu_mul(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(),
+                                              y.stride(0), m, inter, k, _lib.KVH_DTYPE[dtype],
+                                              torch.cuda.current_stream().cuda_stream)  # fmt: skip
+    assert st == 0
+    want = ops.silu_mul(ops.gemm_skinny(x, w))
+    assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+
+
 def test_gemv_strided_rows_and_large_batches_fall_back(hip_device):
     x = torch.randn(3, 4096 + 64, device=hip_device).to(torch.bfloat16)[:, :4096]
     w = torch.randn(512, 4096, device=hip_device).to(torch.bfloat16)

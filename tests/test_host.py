@@ -297,3 +297,22 @@ def _sk(lib, **over):
 )  # fmt: skip
 def test_gemm_skinny_validation(lib, over, status):
     assert _sk(lib, **over) == status
+
+
+@pytest.mark.parametrize(
+    "over,status",
+    [
+        (dict(dtype=0), E_DTYPE),
+        (dict(m=65), E_UNSUPPORTED),
+        (dict(n=6148), E_UNSUPPORTED),  # inter % 8
+        (dict(k=4000), E_UNSUPPORTED),
+        (dict(y=None), E_NULL),
+        (dict(m=0), 0),
+    ],
+)  # fmt: skip
+def test_gemm_skinny_silu_mul_validation(lib, over, status):
+    a = dict(x=0x1000, xs=4096, w=0x2000, ws=4096, y=0x3000, ys=6144, m=8, n=6144, k=4096, dtype=2)
+    a.update(over)
+    st = lib.kvh_gemm_skinny_silu_mul(a["x"], a["xs"], a["w"], a["ws"], a["y"], a["ys"], a["m"], a["n"], a["k"],
+                                      a["dtype"], None)  # fmt: skip
+    assert st == status
