@@ -266,14 +266,15 @@ KVH_API int kvh_gemv(const void* x, int64_t x_row_stride, const void* weight, in
  * projections on weight rows j and inter + j (w_gate_up is [2 * inter, k] row-major), each
  * rounded to dtype, y[i][j] = (silu(g).to(dtype) * u).to(dtype) -- the bits of kvh_gemv then
  * kvh_silu_mul. k % 8 == 0. */
-/* gemv_rope_and_cache: the QKV projection of m <= 4 decode rows followed by
+/* gemv_rope_and_cache: the QKV projection of m <= 64 decode rows followed by
  * kvh_rope_and_cache (kv_fp8 = 0) or kvh_rope_and_cache_fp8 (kv_fp8 != 0) in one launch:
  * qkv = x @ w_qkv^T (w_qkv [(num_heads + 2 num_kv_heads) head_dim, k] row-major, fp32 sums
  * rounded to dtype, as kvh_gemv), then the rotated queries to q_out and the rotated keys and
  * the values to the caches at slot_mapping (slots outside the pool skipped), with the same bits
  * as the two calls in sequence. Replaces the QKV projection and Attention.project + write_kv of
  * a decode step (src/kvserve/model.py:84-94, src/kvserve/attention.py:39-45) at batch sizes
- * where the projection streams its weight; k % 8 == 0, head_dim even. */
+ * where the projection streams its weight; k % 8 == 0, head_dim even (m > 4: the MFMA form,
+ * k % 1024 == 0 and head_dim % 16 == 0). */
 KVH_API int kvh_gemv_rope_and_cache(const void* x, int64_t x_row_stride, const void* w_qkv, int64_t w_row_stride,
                                     int32_t m, int32_t k, const int64_t* positions, const float* cos_table,
                                     const float* sin_table, int64_t max_positions, void* q_out,

@@ -236,8 +236,8 @@ class HipAttention:
             _lib.check(st, "kvh_rope_and_cache")
         return out
 
-    # rows up to which gemv_rope_and_cache applies (the projection then streams its weight)
-    GEMV_ROPE_MAX_ROWS = 4
+    # rows up to which gemv_rope_and_cache applies (up to 4 on the GEMV, then on the MFMA units)
+    GEMV_ROPE_MAX_ROWS = 64
 
     @staticmethod
     def gemv_rope_and_cache(
@@ -255,12 +255,13 @@ class HipAttention:
         v_scale: float = 1.0,
     ) -> torch.Tensor:
         """rope_and_cache(x @ w_qkv.T, ...) in one kernel (kvh_gemv_rope_and_cache) for at most
-        GEMV_ROPE_MAX_ROWS rows of 16-bit x: the same bits as the projection on kvh_gemv
-        followed by rope_and_cache. x: [T, hidden]; w_qkv: [(H + 2 Hkv) D, hidden], contiguous."""
+        GEMV_ROPE_MAX_ROWS rows of 16-bit x: the same bits as the projection on kvh_gemv (up to 4
+        rows) or kvh_gemm_skinny (more; hidden % 1024 == 0, head_dim % 16 == 0) followed by
+        rope_and_cache. x: [T, hidden]; w_qkv: [(H + 2 Hkv) D, hidden], contiguous."""
         num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs = _cache_layout(k_cache, v_cache)
         fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
         num_tokens, hidden = x.shape
-        _require(0 < num_tokens <= HipAttention.GEMV_ROPE_MAX_ROWS, "gemv_rope_and_cache takes 1 .. 4 rows")
+        _require(0 < num_tokens <= HipAttention.GEMV_ROPE_MAX_ROWS, "gemv_rope_and_cache takes 1 .. 64 rows")
         _require(x.stride(-1) == 1 and w_qkv.is_contiguous(), "x needs a contiguous last dim, w_qkv contiguous")
         _require(w_qkv.shape == ((num_heads + 2 * num_kv_heads) * head_dim, hidden), "w_qkv must be [(H + 2 Hkv) D, k]")
         _require(cos.dtype == torch.float32 and sin.dtype == torch.float32, "cos/sin tables must be fp32")

@@ -553,8 +553,9 @@ int kvh_gemv_rope_and_cache(const void* x, int64_t x_row_stride, const void* w_q
   if (m < 0 || k <= 0 || num_blocks < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
       block_size <= 0 || max_positions <= 0)
     return KVH_E_SHAPE;
-  if (m > 4 || k % 8 != 0 || head_dim % 2 != 0 || head_dim > 1024 || num_heads > 65535 || num_kv_heads > 65535)
+  if (m > 64 || k % 8 != 0 || head_dim % 2 != 0 || head_dim > 1024 || num_heads > 65535 || num_kv_heads > 65535)
     return KVH_E_UNSUPPORTED;
+  if (m > 4 && (k % 1024 != 0 || head_dim % 16 != 0)) return KVH_E_UNSUPPORTED;  // the skinny form
   if (m == 0) return KVH_OK;
   if (!x || !w_qkv || !positions || !cos_table || !sin_table || !q_out || !k_cache || !v_cache || !k_cache_strides ||
       !v_cache_strides || !slot_mapping)

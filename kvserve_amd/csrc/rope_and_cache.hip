@@ -216,6 +216,41 @@ __device__ __forceinline__ void store_one(uint8_t* dst, float x, float scale) {
   }
 }
 
+// rope_and_cache of one pair (d, d + D / 2) of head h for token row `row`, from the two fp32
+// projection sums
+template <int DT, bool KV8>
+__device__ __forceinline__ void rope_pair_out(const GemvRopeArgs& a, int row, int h, int d, float s_lo, float s_hi) {
+  using R = RopeElem<DT>;
+  constexpr int CB = KV8 ? 1 : 2;  // bytes per cache element
+  const int half = a.D / 2;
+  const float lo = R::rnd(s_lo), hi = R::rnd(s_hi);  // the projection's output
+  const int64_t slot = a.slots[row];
+  const bool in_pool = slot >= 0 && slot < a.num_slots;
+  const int64_t blk = in_pool ? slot / a.BS : 0, off = in_pool ? slot % a.BS : 0;
+  if (h < a.H + a.Hkv) {
+    const int64_t pos = clamp64(a.positions[row], 0, a.max_pos - 1);
+    const float* cr = a.cos_t + pos * a.D;
+    const float* sr = a.sin_t + pos * a.D;
+    const float c_lo = R::rnd(cr[d]), c_hi = R::rnd(cr[d + half]);
+    const float s_lo2 = R::rnd(sr[d]), s_hi2 = R::rnd(sr[d + half]);
+    const float o_lo = R::add(R::mul(lo, c_lo), R::mul(-hi, s_lo2));
+    const float o_hi = R::add(R::mul(hi, c_hi), R::mul(lo, s_hi2));
+    if (h < a.H) {
+      uint8_t* dst = a.q_out + (row * a.q_ts + (int64_t)h * a.q_hs + d) * 2;
+      store_one<DT, false>(dst, o_lo, 1.f);
+      store_one<DT, false>(dst + half * 2, o_hi, 1.f);
+    } else if (in_pool) {
+      uint8_t* dst = a.kc + (blk * a.k_sb + off * a.k_ss + (int64_t)(h - a.H) * a.k_sh + d) * CB;
+      store_one<DT, KV8>(dst, o_lo, a.k_scale);
+      store_one<DT, KV8>(dst + half * CB, o_hi, a.k_scale);
+    }
+  } else if (in_pool) {
+    uint8_t* dst = a.vc + (blk * a.v_sb + off * a.v_ss + (int64_t)(h - a.H - a.Hkv) * a.v_sh + d) * CB;
+    store_one<DT, KV8>(dst, lo, a.v_scale);
+    store_one<DT, KV8>(dst + half * CB, hi, a.v_scale);
+  }
+}
+
 template <int DT, int M, bool KV8>
 __global__ __launch_bounds__(256) void gemv_rope_cache_kernel(GemvRopeArgs a) {
   using R = RopeElem<DT>;
@@ -274,39 +309,76 @@ __global__ __launch_bounds__(256) void gemv_rope_cache_kernel(GemvRopeArgs a) {
     }
   if (lane != 0) return;
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    const float lo = R::rnd(acc[m][0]), hi = R::rnd(acc[m][1]);  // the projection's output
-    const int64_t slot = a.slots[m];
-    const bool in_pool = slot >= 0 && slot < a.num_slots;
-    const int64_t blk = in_pool ? slot / a.BS : 0, off = in_pool ? slot % a.BS : 0;
-    if (h < a.H + a.Hkv) {
-      const int64_t pos = clamp64(a.positions[m], 0, a.max_pos - 1);
-      const float* cr = a.cos_t + pos * a.D;
-      const float* sr = a.sin_t + pos * a.D;
-      const float c_lo = R::rnd(cr[d]), c_hi = R::rnd(cr[d + half]);
-      const float s_lo = R::rnd(sr[d]), s_hi = R::rnd(sr[d + half]);
-      const float o_lo = R::add(R::mul(lo, c_lo), R::mul(-hi, s_lo));
-      const float o_hi = R::add(R::mul(hi, c_hi), R::mul(lo, s_hi));
-      if (h < a.H) {
-        uint8_t* dst = a.q_out + (m * a.q_ts + (int64_t)h * a.q_hs + d) * 2;
-        store_one<DT, false>(dst, o_lo, 1.f);
-        store_one<DT, false>(dst + half * 2, o_hi, 1.f);
-      } else if (in_pool) {
-        uint8_t* dst = a.kc + (blk * a.k_sb + off * a.k_ss + (int64_t)(h - a.H) * a.k_sh + d) * CB;
-        store_one<DT, KV8>(dst, o_lo, a.k_scale);
-        store_one<DT, KV8>(dst + half * CB, o_hi, a.k_scale);
-      }
-    } else if (in_pool) {
-      uint8_t* dst = a.vc + (blk * a.v_sb + off * a.v_ss + (int64_t)(h - a.H - a.Hkv) * a.v_sh + d) * CB;
-      store_one<DT, KV8>(dst, lo, a.v_scale);
-      store_one<DT, KV8>(dst + half * CB, hi, a.v_scale);
+  for (int m = 0; m < M; ++m) rope_pair_out<DT, KV8>(a, m, h, d, acc[m][0], acc[m][1]);
+}
+
+// The same for 5 .. 64 rows on the MFMA units, laid out as the skinny GEMM (engine_ops.hip):
+// a workgroup of 8 waves (k-slices) owns 8 pairs (one 16-row A tile: rows h D + d0 + i for
+// i < 8, h D + d0 + D / 2 + i - 8 for i >= 8) and MT = ceil(m / 16) B tiles of x; the eight
+// partial tiles meet in LDS, are summed in wave order and go through rope_pair_out.
+template <int DT, int MT, bool KV8>
+__global__ __launch_bounds__(512) void skinny_rope_cache_kernel(GemvRopeArgs a, int m) {
+  using E = std::conditional_t<DT == 2, BF16, F16>;
+  __shared__ f32x4 red[8][MT][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = lane & 15, jg = lane >> 4;
+  const int half = a.D / 2;
+  const int p0 = blockIdx.x * 8;  // first pair
+  const int h = p0 / half, d0 = p0 % half;
+  const int64_t wrow = (int64_t)h * a.D + d0 + (i < 8 ? i : half + i - 8);
+  const int slice = a.k / 8;
+  const int k_lo = wave * slice;
+  const uint16_t* wr = a.w + wrow * a.w_rs + k_lo + 8 * jg;
+  const uint16_t* xr[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) xr[t] = a.x + (int64_t)min(16 * t + i, m - 1) * a.x_rs + k_lo + 8 * jg;
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int kk = 0; kk < slice; kk += 128) {
+    u32x4 av[4], bv[4][MT];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      av[u] = *(const u32x4*)(wr + kk + 32 * u);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) bv[u][t] = *(const u32x4*)(xr[t] + kk + 32 * u);
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[t] = E::mfma(av[u], bv[u][t], acc[t]);
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
+  __syncthreads();
+  for (int q = threadIdx.x; q < MT * 128; q += 512) {
+    const int t = q >> 7, mr = (q >> 3) & 15, c = q & 7;
+    const int row = 16 * t + mr;
+    if (row >= m) continue;
+    const int ll = 16 * (c >> 2) + mr, lh = 16 * (2 + (c >> 2)) + mr, r = c & 3;
+    float s_lo = 0.f, s_hi = 0.f;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      s_lo += red[v][t][ll][r];
+      s_hi += red[v][t][lh][r];
+    }
+    rope_pair_out<DT, KV8>(a, row, h, d0 + c, s_lo, s_hi);
   }
 }
 
 template <int DT, bool KV8>
 static int launch_gemv_rope_dt(const GemvRopeArgs& a, int m, hipStream_t s) {
   const int waves = (a.H + 2 * a.Hkv) * (a.D / 2);
+  if (m > 4) {  // the skinny form: one workgroup per 8 pairs
+    const dim3 g2((unsigned)(waves / 8)), b2(512);
+    switch ((m + 15) / 16) {
+      case 1: hipLaunchKernelGGL((skinny_rope_cache_kernel<DT, 1, KV8>), g2, b2, 0, s, a, m); break;
+      case 2: hipLaunchKernelGGL((skinny_rope_cache_kernel<DT, 2, KV8>), g2, b2, 0, s, a, m); break;
+      case 3: hipLaunchKernelGGL((skinny_rope_cache_kernel<DT, 3, KV8>), g2, b2, 0, s, a, m); break;
+      default: hipLaunchKernelGGL((skinny_rope_cache_kernel<DT, 4, KV8>), g2, b2, 0, s, a, m); break;
+    }
+    return (int)hipGetLastError();
+  }
   const dim3 grid((waves + 3) / 4);
   switch (m) {
     case 1: hipLaunchKernelGGL((gemv_rope_cache_kernel<DT, 1, KV8>), grid, dim3(256), 0, s, a); break;

@@ -233,7 +233,7 @@ class LlamaForCausalLM(nn.Module):
             if i == n:
                 return h, None, None, None
         layer = self.layers[i]
-        if self.fused_rope and self._gemv_rope and 0 < h.shape[0] <= self.backend.GEMV_ROPE_MAX_ROWS:
+        if self.fused_rope and self._gemv_rope and ops.qkv_rope_fused(h.shape[0], *layer.self_attn.qkv_proj.weight.shape):
             return x, None, h, None  # the projection runs in the attention step (gemv_rope_and_cache)
         qkv = ops.linear(h, layer.self_attn.qkv_proj.weight)
         if self.fused_rope:

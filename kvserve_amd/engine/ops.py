@@ -64,6 +64,12 @@ def skinny_wins(m: int, n: int, k: int) -> bool:
     return m <= 32 and w_bytes <= 13e6
 
 
+def qkv_rope_fused(m: int, n: int, k: int) -> bool:
+    """Whether the QKV projection of m rows runs fused with RoPE + cache write
+    (gemv_rope_and_cache): where the projection would take the GEMV or the skinny GEMM."""
+    return 0 < m <= GEMV_MAX_ROWS or (m > GEMV_MAX_ROWS and skinny_wins(m, n, k))
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """x @ weight.T: kvh_gemv for at most GEMV_MAX_ROWS rows, kvh_gemm_skinny where it beats
     hipBLASLt (skinny_wins), else PyTorch (hipBLASLt)."""

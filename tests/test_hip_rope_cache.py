@@ -88,13 +88,15 @@ def test_argument_errors(hip_device):
 
 # -- the QKV projection fused with RoPE + cache write (kvh_gemv_rope_and_cache) ----------------
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
-@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 17])
 @pytest.mark.parametrize("H,Hkv,D,k", [(32, 8, 128, 4096), (32, 8, 64, 2048), (8, 2, 64, 136)])
 @pytest.mark.parametrize("fp8", [False, True], ids=["cache16", "e4m3"])
 def test_gemv_rope_and_cache_is_gemv_then_rope_and_cache(hip_device, dtype, m, H, Hkv, D, k, fp8):
-    """The fused kernel gives the bits of the projection on kvh_gemv followed by
-    rope_and_cache: the same q, the same cache bytes (16-bit or E4M3 with scales), slots
-    outside the pool skipped; k = 136 runs the projection's tail loop."""
+    """The fused kernel gives the bits of the projection on kvh_gemv (m <= 4) or kvh_gemm_skinny
+    (m > 4) followed by rope_and_cache: the same q, the same cache bytes (16-bit or E4M3 with
+    scales), slots outside the pool skipped; k = 136 runs the GEMV's tail loop."""
+    if m > 4 and k % 1024:
+        pytest.skip("the MFMA form takes k % 1024 == 0")
     from kvserve_amd.engine import ops
     from oracle import fp8 as fp8_oracle
 
@@ -114,7 +116,8 @@ def test_gemv_rope_and_cache_is_gemv_then_rope_and_cache(hip_device, dtype, m, H
         kc, vc = fp8_oracle.quantize(kc, 1.0).to(hip_device), fp8_oracle.quantize(vc, 1.0).to(hip_device)
     kc2, vc2 = kc.clone(), vc.clone()
     got = HipAttention.gemv_rope_and_cache(x, w, pos, rope.cos, rope.sin, kc, vc, slots, H, **sc)
-    want = HipAttention.rope_and_cache(ops.gemv(x, w), pos, rope.cos, rope.sin, kc2, vc2, slots, H, **sc)
+    proj = ops.gemv(x, w) if m <= 4 else ops.gemm_skinny(x, w)
+    want = HipAttention.rope_and_cache(proj, pos, rope.cos, rope.sin, kc2, vc2, slots, H, **sc)
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
     assert torch.equal(kc.view(torch.uint8), kc2.view(torch.uint8))

@@ -260,7 +260,8 @@ def _gr(lib, **over):
     [
         (dict(dtype=0), E_DTYPE),
         (dict(fp8=1, ks=0.0), E_SHAPE),
-        (dict(m=5), E_UNSUPPORTED),
+        (dict(m=65), E_UNSUPPORTED),
+        (dict(m=5, k=1032, xs=1032, ws=1032), E_UNSUPPORTED),
         (dict(D=63), E_UNSUPPORTED),
         (dict(k=100), E_UNSUPPORTED),
         (dict(slots=None), E_NULL),
