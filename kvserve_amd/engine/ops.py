@@ -66,8 +66,17 @@ def skinny_wins(m: int, n: int, k: int) -> bool:
 
 def qkv_rope_fused(m: int, n: int, k: int) -> bool:
     """Whether the QKV projection of m rows runs fused with RoPE + cache write
-    (gemv_rope_and_cache): where the projection would take the GEMV or the skinny GEMM."""
-    return 0 < m <= GEMV_MAX_ROWS or (m > GEMV_MAX_ROWS and skinny_wins(m, n, k))
+    (gemv_rope_and_cache; the GEMV up to 4 rows, the skinny MFMA form above). The fusion saves
+    the separate rope_and_cache launch and the qkv round trip, so it pays past skinny_wins's
+    limits (measured inside the decode graph): up to 64 rows for weights up to 13 MB (1B QKV:
+    batch 48 +4-7%, batch 64 +2-3% against hipBLASLt + rope_and_cache) and up to 16 rows for
+    weights up to 80 MB (8B QKV; at 32 rows -3%, at 64 rows -9%)."""
+    if 0 < m <= GEMV_MAX_ROWS:
+        return True
+    if m > 64 or n % 16 or k % 1024:
+        return False
+    w_bytes = 2 * n * k
+    return w_bytes <= 13e6 or (m <= 16 and w_bytes <= 80e6)
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:

@@ -154,7 +154,7 @@ def test_fused_model_matches_the_unfused_model(hip_device):
             with torch.inference_mode():
                 x, qkv, h0, _ = mdl.piece(0, ids, None, None, None)
                 if qkv is None:  # decode-sized: the projection runs in the attention step
-                    qkv = ops.gemv(h0, mdl.layers[0].self_attn.qkv_proj.weight)
+                    qkv = ops.linear(h0, mdl.layers[0].self_attn.qkv_proj.weight)
                 attn = qkv[:, : cfg.num_heads * cfg.head_dim].reshape(T, cfg.num_heads, cfg.head_dim)
                 h, _, _, _ = mdl.piece(1, ids, None, x, attn)
                 x2, _, _, _ = mdl.piece(2, ids, None, h, attn)

@@ -88,7 +88,7 @@ def test_argument_errors(hip_device):
 
 # -- the QKV projection fused with RoPE + cache write (kvh_gemv_rope_and_cache) ----------------
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 17])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 17, 33, 64])
 @pytest.mark.parametrize("H,Hkv,D,k", [(32, 8, 128, 4096), (32, 8, 64, 2048), (8, 2, 64, 136)])
 @pytest.mark.parametrize("fp8", [False, True], ids=["cache16", "e4m3"])
 def test_gemv_rope_and_cache_is_gemv_then_rope_and_cache(hip_device, dtype, m, H, Hkv, D, k, fp8):
