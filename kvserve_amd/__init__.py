@@ -17,6 +17,7 @@ from kvserve_amd.attention import (
     build_metadata,
     get_backend,
     hip_available,
+    hip_eligible,
     last_launch_kernels,
 )
 
@@ -26,5 +27,6 @@ __all__ = [
     "build_metadata",
     "get_backend",
     "hip_available",
+    "hip_eligible",
     "last_launch_kernels",
 ]

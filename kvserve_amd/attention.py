@@ -5,8 +5,9 @@ Mirrors src/kvserve/attention.py of the reference:
   * `HipAttention` is a class used as a namespace of static methods with the exact
     `write_kv` / `forward` signatures of the reference's backends (attention.py:39-82,
     :88-102), so `Attention.attend` (model.py:96-108) calls it unchanged;
-  * `get_backend(name, device, block_size)` keeps the reference's selector contract
-    (attention.py:113-124) for the names this package serves ("hip", "auto").
+  * `get_backend(name, device, block_size, fallback)` keeps the reference's selector contract
+    (attention.py:113-124) for the names this package serves ("hip", and "auto", which
+    falls back instead of raising).
 
 Both methods run on `torch.cuda.current_stream()`, allocate only through torch's caching
 allocator (the output when `out is None`, and the split-K workspace), never synchronise
@@ -76,17 +77,27 @@ _WS_SIZES: dict = {}
 
 
 def _cache_layout(k_cache: torch.Tensor, v_cache: torch.Tensor) -> tuple:
+    """(num_blocks, block_size, kv_heads, head_dim, k strides, v strides, device index)."""
     ks, vs = k_cache.stride(), v_cache.stride()
     key = (k_cache.data_ptr(), v_cache.data_ptr(), k_cache.get_device(), v_cache.get_device(), k_cache.dtype,
            v_cache.dtype, k_cache.shape, v_cache.shape, ks, vs)  # fmt: skip
     hit = _CACHE_LAYOUTS.get(key)
     if hit is None:
         _check_cache(k_cache, v_cache)
+        _require(k_cache.get_device() == v_cache.get_device(), "k_cache and v_cache are on different devices")
         if len(_CACHE_LAYOUTS) > 256:
             _CACHE_LAYOUTS.clear()
-        hit = (*k_cache.shape, _lib.i64x3(ks[:3]), _lib.i64x3(vs[:3]))
+        hit = (*k_cache.shape, _lib.i64x3(ks[:3]), _lib.i64x3(vs[:3]), k_cache.get_device())
         _CACHE_LAYOUTS[key] = hit
     return hit
+
+
+def _on_device(dev: int, **tensors: torch.Tensor) -> None:
+    """Every tensor argument lives on the caches' device: a host tensor's address handed to a
+    kernel would be a GPU memory fault, not an error."""
+    for name, t in tensors.items():
+        if t.get_device() != dev:
+            raise ValueError(f"{name} must be on the caches' device cuda:{dev} (got {t.device})")
 
 
 def _workspace_size(lib, *shape) -> int:
@@ -116,7 +127,6 @@ def _kv_format(k_cache: torch.Tensor, v_cache: torch.Tensor, k_scale: float, v_s
 
 def _check_index(t: torch.Tensor, name: str, dim: int) -> None:
     _require(t.dtype == torch.int64, f"{name} must be int64 (got {t.dtype})")
-    _require(t.is_cuda, f"{name} must be on the device")
     _require(t.dim() == dim and t.stride(-1) == 1, f"{name} must be {dim}-d with a contiguous last dim")
 
 
@@ -151,8 +161,9 @@ class HipAttention:
         Slots outside the pool are skipped instead of raising. float8_e4m3fn caches store
         (x / scale).clamp(-448, 448).to(float8_e4m3fn) with the given scales, bit for bit.
         """
-        num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs = _cache_layout(k_cache, v_cache)
+        num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs, dev = _cache_layout(k_cache, v_cache)
         fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
+        _on_device(dev, k=k, v=v, slot_mapping=slots)
         _require(k.dim() == 3 and k.shape == v.shape, "k and v must be [T, kv_heads, head_dim]")
         _require(k.shape[1:] == (num_kv_heads, head_dim), f"k/v rows {tuple(k.shape[1:])} != cache rows")
         _require(k.stride(-1) == 1 and v.stride(-1) == 1, "k/v last dim must be contiguous")
@@ -204,8 +215,9 @@ class HipAttention:
         RoPE(q) as [T, num_heads, head_dim] (in `out` if given), bit-identical to the
         reference's bf16/fp16/fp32 torch operations.
         """
-        num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs = _cache_layout(k_cache, v_cache)
+        num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs, dev = _cache_layout(k_cache, v_cache)
         fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
+        _on_device(dev, qkv=qkv, positions=positions, cos=cos, sin=sin, slot_mapping=slots)
         _require(qkv.dim() == 2 and qkv.stride(-1) == 1, "qkv must be [T, (H + 2 Hkv) D] with a contiguous last dim")
         _require(qkv.shape[1] == (num_heads + 2 * num_kv_heads) * head_dim, "qkv width != (H + 2 Hkv) D")
         _require(cos.dtype == torch.float32 and sin.dtype == torch.float32, "cos/sin tables must be fp32")
@@ -217,6 +229,7 @@ class HipAttention:
         _require(positions.shape[0] == num_tokens and slots.shape[0] == num_tokens, "one position and slot per token")
         if out is None:
             out = torch.empty((num_tokens, num_heads, head_dim), dtype=qkv.dtype, device=qkv.device)
+        _on_device(dev, out=out)
         _require(out.shape == (num_tokens, num_heads, head_dim) and out.stride(-1) == 1, "out must be [T, H, D]")
         dtype = _dtype_code(qkv, out) if fp8 else _dtype_code(qkv, k_cache, v_cache, out)
         if num_tokens == 0:
@@ -258,8 +271,10 @@ class HipAttention:
         GEMV_ROPE_MAX_ROWS rows of 16-bit x: the same bits as the projection on kvh_gemv (up to 4
         rows) or kvh_gemm_skinny (more; hidden % 1024 == 0, head_dim % 16 == 0) followed by
         rope_and_cache. x: [T, hidden]; w_qkv: [(H + 2 Hkv) D, hidden], contiguous."""
-        num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs = _cache_layout(k_cache, v_cache)
+        num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs, dev = _cache_layout(k_cache, v_cache)
         fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
+        _on_device(dev, x=x, w_qkv=w_qkv, positions=positions, cos=cos, sin=sin, slot_mapping=slots)
+        _require(x.dim() == 2, "x must be [T, hidden]")
         num_tokens, hidden = x.shape
         _require(0 < num_tokens <= HipAttention.GEMV_ROPE_MAX_ROWS, "gemv_rope_and_cache takes 1 .. 64 rows")
         _require(x.stride(-1) == 1 and w_qkv.is_contiguous(), "x needs a contiguous last dim, w_qkv contiguous")
@@ -272,6 +287,7 @@ class HipAttention:
         _require(positions.shape[0] == num_tokens and slots.shape[0] == num_tokens, "one position and slot per token")
         if out is None:
             out = torch.empty((num_tokens, num_heads, head_dim), dtype=x.dtype, device=x.device)
+        _on_device(dev, out=out)
         _require(out.shape == (num_tokens, num_heads, head_dim) and out.stride(-1) == 1, "out must be [T, H, D]")
         dtype = _dtype_code(x, w_qkv, out) if fp8 else _dtype_code(x, w_qkv, k_cache, v_cache, out)
         st = _lib.load().kvh_gemv_rope_and_cache(
@@ -298,13 +314,14 @@ class HipAttention:
     ) -> torch.Tensor:
         """q: [T, H, D]; caches: [num_blocks, block_size, H_kv, D]. Returns [T, H, D] (in `out` if given).
         float8_e4m3fn caches hold keys / values as e4m3 * k_scale / v_scale (q and out bf16 or fp16)."""
-        num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs = _cache_layout(k_cache, v_cache)
+        num_blocks, block_size, num_kv_heads, head_dim, kcs, vcs, dev = _cache_layout(k_cache, v_cache)
         fp8 = _kv_format(k_cache, v_cache, k_scale, v_scale)
+        tables, seq_lens, qsl = meta.block_tables, meta.seq_lens, meta.query_start_loc
+        _on_device(dev, q=q, block_tables=tables, seq_lens=seq_lens, query_start_loc=qsl)
         _require(q.dim() == 3 and q.shape[2] == head_dim, "q must be [T, H, head_dim]")
         _require(q.stride(-1) == 1, "q last dim must be contiguous")
         num_tokens, num_heads, _ = q.shape
         _require(num_heads % num_kv_heads == 0, "num_heads must be a multiple of num_kv_heads")
-        tables, seq_lens, qsl = meta.block_tables, meta.seq_lens, meta.query_start_loc
         _check_index(tables, "block_tables", 2)
         _check_index(seq_lens, "seq_lens", 1)
         _check_index(qsl, "query_start_loc", 1)
@@ -312,6 +329,7 @@ class HipAttention:
         _require(seq_lens.shape[0] == num_seqs and qsl.shape[0] == num_seqs + 1, "metadata sizes disagree")
         if out is None:
             out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        _on_device(dev, out=out)
         _require(out.shape == q.shape and out.stride(-1) == 1, "out must match q with a contiguous last dim")
         dtype = _dtype_code(q, out) if fp8 else _dtype_code(q, k_cache, v_cache, out)
         _require(not fp8 or q.dtype != torch.float32, "float8_e4m3fn caches need bf16 or fp16 queries")
@@ -360,18 +378,24 @@ def hip_available() -> bool:
     return True
 
 
-def get_backend(name: str, device: str, block_size: int) -> type[HipAttention]:
+def hip_eligible(device: str, block_size: int) -> bool:
+    """True when the HIP backend can serve this engine: a ROCm device, libkvhip loaded and a
+    block size the 16-token MFMA tiles divide."""
+    return str(device).startswith("cuda") and block_size >= 16 and block_size % 16 == 0 and hip_available()
+
+
+def get_backend(name: str, device: str, block_size: int, fallback=None):
     """Selector with the reference's contract (src/kvserve/attention.py:113-124).
 
-    "hip" (and "auto" on a ROCm device) -> HipAttention. The reference's "torch" and
-    "triton" names stay with the reference's own classes; this package does not ship a
-    CPU path. Errors mirror the reference: RuntimeError when the backend cannot run,
-    ValueError for an unsupported block size or an unknown name.
+    "auto" never raises, as in the reference: it resolves to HipAttention when the backend can
+    run here (`hip_eligible`), otherwise to `fallback` -- the backend the caller's own "auto"
+    would pick (kvserve passes its torch / triton choice; None when not given). "hip" raises
+    RuntimeError when the backend cannot run and ValueError for a block size the kernels do
+    not tile, like the reference's "triton". The reference's "torch" and "triton" names stay
+    with its own classes: this package ships no CPU path.
     """
     if name == "auto":
-        if not (device.startswith("cuda") and hip_available()):
-            raise RuntimeError("auto: no ROCm GPU + libkvhip here; select kvserve's own 'torch' backend instead")
-        name = "hip"
+        return HipAttention if hip_eligible(device, block_size) else fallback
     if name == "hip":
         if not hip_available():
             raise RuntimeError("hip backend needs a ROCm GPU and a built kvserve_amd/lib/libkvhip.so")

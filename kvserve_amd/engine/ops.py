@@ -25,9 +25,17 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+def _same_gpu(*tensors: torch.Tensor) -> None:
+    """All arguments on one GPU: a host tensor's address in a kernel would fault the GPU."""
+    dev = tensors[0].get_device()
+    if dev < 0 or any(t.get_device() != dev for t in tensors):
+        raise ValueError(f"libkvhip kernels need every tensor on one GPU (got {[str(t.device) for t in tensors]})")
+
+
 def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tensor,
                 eps: float) -> tuple[torch.Tensor, torch.Tensor]:  # fmt: skip
     """(x + delta, RMSNorm(x + delta)) for [T, hidden] rows; with delta None, (x, RMSNorm(x))."""
+    _same_gpu(x, weight, *([delta] if delta is not None else []))
     T, hd = x.shape
     h = torch.empty_like(x)
     xo = torch.empty_like(x) if delta is not None else x
@@ -41,6 +49,7 @@ def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tenso
 
 
 def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    _same_gpu(gate_up)
     T, two_i = gate_up.shape
     out = torch.empty((T, two_i // 2), dtype=gate_up.dtype, device=gate_up.device)
     st = _lib.load().kvh_silu_mul(gate_up.data_ptr(), gate_up.stride(0), out.data_ptr(), out.stride(0), T, two_i // 2,
@@ -94,6 +103,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
 
 def gemm_skinny(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """x @ weight.T on kvh_gemm_skinny (x: at most 64 rows; n % 16 == 0, k % 1024 == 0)."""
+    _same_gpu(x, weight)
     m = x.shape[0]
     n, k = weight.shape
     y = torch.empty((m, n), dtype=x.dtype, device=x.device)
@@ -109,6 +119,7 @@ def mlp_act(x: torch.Tensor, gate_up_weight: torch.Tensor) -> torch.Tensor:
     m = x.shape[0]
     if m == 0 or x.stride(-1) != 1 or not gate_up_weight.is_contiguous():
         return silu_mul(linear(x, gate_up_weight))
+    _same_gpu(x, gate_up_weight)
     if m > GEMV_MAX_ROWS:
         two_i, k = gate_up_weight.shape
         if two_i % 16 or not skinny_wins(m, two_i, k):
@@ -130,6 +141,7 @@ def mlp_act(x: torch.Tensor, gate_up_weight: torch.Tensor) -> torch.Tensor:
 
 def gemv(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """x @ weight.T on kvh_gemv (x: at most 8 rows, unit stride in k; weight contiguous)."""
+    _same_gpu(x, weight)
     m = x.shape[0]
     n, k = weight.shape
     y = torch.empty((m, n), dtype=x.dtype, device=x.device)

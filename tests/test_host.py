@@ -134,22 +134,65 @@ def test_workspace_follows_the_plan(lib):
 
 
 def test_get_backend_contract(monkeypatch):
+    """The reference's selector (attention.py:113-124): "auto" never raises -- it falls back
+    when the backend cannot run or the block size does not tile; "hip" raises RuntimeError /
+    ValueError like "triton"; unknown names raise ValueError."""
+    fallback = object()
     with pytest.raises(ValueError):
         attention.get_backend("torch", "cuda", 16)
     with pytest.raises(ValueError):
         attention.get_backend("nope", "cuda", 16)
+    assert attention.get_backend("auto", "cpu", 16, fallback=fallback) is fallback
+    assert attention.get_backend("auto", "cpu", 16) is None
     if not attention.hip_available():
         with pytest.raises(RuntimeError):
             attention.get_backend("hip", "cuda", 16)
-        with pytest.raises(RuntimeError):
-            attention.get_backend("auto", "cpu", 16)
+        assert attention.get_backend("auto", "cuda", 16, fallback=fallback) is fallback
     monkeypatch.setattr(attention, "hip_available", lambda: True)
     assert attention.get_backend("hip", "cuda", 16) is attention.HipAttention
     assert attention.get_backend("auto", "cuda", 32) is attention.HipAttention
-    with pytest.raises(ValueError):
-        attention.get_backend("hip", "cuda", 8)
+    assert attention.get_backend("auto", "cuda:0", 16, fallback=fallback) is attention.HipAttention
+    for bs in (8, 24, 4):  # blocks the 16-token tiles do not divide
+        assert attention.get_backend("auto", "cuda", bs, fallback=fallback) is fallback
+        with pytest.raises(ValueError):
+            attention.get_backend("hip", "cuda", bs)
+    assert attention.get_backend("auto", "cpu", 16, fallback=fallback) is fallback
     cls = attention.HipAttention
     assert cls.graph_capturable and not cls.needs_padded_layout
+
+
+class _NoLib:
+    """Stands in for the loaded library: any attribute access is a failure."""
+
+    def __getattr__(self, name):
+        raise AssertionError(f"{name} reached the library with a host tensor argument")
+
+
+def test_host_tensors_are_rejected_before_the_library(monkeypatch):
+    """A CPU tensor's address must never reach a kernel: every tensor argument is checked
+    against the caches' device before any library call (a GPU memory fault otherwise)."""
+    monkeypatch.setattr(attention._lib, "load", lambda: _NoLib())
+    monkeypatch.setattr(attention, "_workspace_size", lambda *a: 0)
+    T, H, Hkv, D, BS, NB = 4, 8, 2, 64, 16, 8
+    layout = (NB, BS, Hkv, D, _lib.i64x3((BS * Hkv * D, Hkv * D, D)), _lib.i64x3((BS * Hkv * D, Hkv * D, D)), 0)
+    monkeypatch.setattr(attention, "_cache_layout", lambda kc, vc: layout)
+    kc = torch.zeros(NB, BS, Hkv, D, dtype=torch.bfloat16)
+    q = torch.zeros(T, H, D, dtype=torch.bfloat16)
+    k = torch.zeros(T, Hkv, D, dtype=torch.bfloat16)
+    slots = torch.arange(T)
+    meta = attention.build_metadata("cpu", [[0]], slots.tolist(), [T], [T])
+    with pytest.raises(ValueError, match="device"):
+        attention.HipAttention.forward(q, kc, kc, meta, 0.125)
+    with pytest.raises(ValueError, match="device"):
+        attention.HipAttention.write_kv(kc, kc, k, k, slots)
+    qkv = torch.zeros(T, (H + 2 * Hkv) * D, dtype=torch.bfloat16)
+    cos = torch.zeros(64, D)
+    with pytest.raises(ValueError, match="device"):
+        attention.HipAttention.rope_and_cache(qkv, slots, cos, cos, kc, kc, slots, H)
+    x = torch.zeros(T, 256, dtype=torch.bfloat16)
+    w = torch.zeros((H + 2 * Hkv) * D, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="device"):
+        attention.HipAttention.gemv_rope_and_cache(x, w, slots, cos, cos, kc, kc, slots, H)
 
 
 def test_build_metadata_layout():
