@@ -263,3 +263,43 @@ def test_argument_errors_raise(hip_device):
     bad = torch.empty(b.k_cache.shape[:3] + (96,), dtype=torch.bfloat16, device=hip_device)
     with pytest.raises((ValueError, RuntimeError)):
         HipAttention.forward(b.q[..., :96].contiguous(), bad, bad, b.meta, w.scale)
+
+
+@pytest.mark.parametrize("block_size", [32, 64])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_prefill_class_large_blocks(hip_device, block_size, head_dim, dtype):
+    """Prefill-class queries (q_len * G > 64) over 16-bit caches with 32- and 64-token pages:
+    the prefill kernel's chunks cross page boundaries inside a page, next to decode rows."""
+    w = workloads.custom(f"pre_bs{block_size}", [40, 1, 100, 17, 1], [70, 500, 0, 1000, 33], 32, 8, head_dim,
+                         block_size, seed=11)  # fmt: skip
+    b = workloads.materialize(w, dtype, hip_device, seed=11)
+    out = pc.attend(b)
+    kinds = last_launch_kernels()
+    assert "prefill" in kinds, kinds
+    assert pc.written_rows_match(b)
+    err = (out.float().cpu() - pc.torch_oracle_full(b)).abs().max().item()
+    assert err <= pc.TOL_16BIT, f"BS {block_size} D {head_dim} {dtype}: {err}"
+
+
+@pytest.mark.parametrize(
+    ("heads", "q_lens", "ctx_lens"),
+    [
+        ((32, 1), [1] * 6, [5, 300, 17, 1000, 64, 2]),  # G=32 decode: two 16-row tiles per kv head
+        ((32, 1), [2, 1, 2], [400, 90, 3]),  # G=32 verify: 64 rows, four tiles, decode class
+        ((32, 1), [1, 40, 1, 9], [700, 30, 2, 0]),  # G=32 mixed: prefill tiles of 4 tokens
+        ((64, 1), [1] * 4, [33, 800, 1, 250]),  # G=64 decode: four tiles per kv head
+        ((64, 2), [1, 20, 1], [500, 60, 7]),  # G=64 mixed: prefill tiles of 2 tokens
+    ],
+    ids=["g32_decode", "g32_verify", "g32_mixed", "g64_decode", "g64_mixed"],
+)
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_wide_gqa_groups(hip_device, heads, q_lens, ctx_lens, dtype):
+    """GQA groups of 32 and 64 query heads per kv head (the largest the C ABI accepts)."""
+    H, Hkv = heads
+    w = workloads.custom("wide_g", q_lens, ctx_lens, H, Hkv, 128, 16, seed=12)
+    b = workloads.materialize(w, dtype, hip_device, seed=12)
+    out = pc.attend(b)
+    assert torch.isfinite(out.float()).all()
+    err = (out.float().cpu() - pc.torch_oracle_full(b)).abs().max().item()
+    assert err <= pc.TOL_16BIT, f"{heads} {q_lens}: {err} ({last_launch_kernels()})"
