@@ -54,6 +54,7 @@ enum kvh_status {
   KVH_E_ALIGN = -4,       /* pointer/stride not aligned for the vector kernels */
   KVH_E_UNSUPPORTED = -5, /* valid, but not a head_dim/block_size/GQA combination built here */
   KVH_E_WORKSPACE = -6,   /* workspace missing or smaller than kvh_paged_attention_workspace_size() */
+  KVH_E_SCRATCH = -7,     /* kvh_paged_attention_static: the launch needs more than KVH_STATIC_SCRATCH_BYTES */
 };
 
 /* ABI version this library was built with (KVH_ABI_VERSION). */
@@ -215,6 +216,34 @@ KVH_API int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_h
                         int64_t num_tokens, int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
                         int32_t head_dim, int32_t block_size, int32_t max_query_len, float scale,
                         int32_t dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * kvh_paged_attention_static: kvh_paged_attention without a workspace argument and without
+ * any allocation. No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops and harnesses that forbid
+ * hipMalloc); the caller passes only inputs and outputs. The split-K workspace is a static
+ * device array of this library, KVH_STATIC_SCRATCH_BYTES (256 MiB) per device, held by every
+ * device the library runs on until the process ends. Launches whose workspace
+ * (kvh_paged_attention_workspace_size) exceeds it return KVH_E_SCRATCH before any GPU work.
+ * At 8 kv heads x 128 (bf16) that admits decode batches of up to ~7k sequences, 5-token
+ * verify of up to ~1.4k sequences and mixed prefill + decode steps with up to ~1.4k
+ * sequences (the 2048-token step of 4 prefills and 512 decodes needs 205 MB).
+ * Results are those of kvh_paged_attention on the same inputs, bit for bit.
+ * All calls on one device share its array and nothing in it needs clearing between calls;
+ * calls that overlap in time on one device (several host threads, or streams that do not
+ * serialise) race on it. The stream must belong to the current device.
+ */
+#define KVH_STATIC_SCRATCH_BYTES (256u << 20)
+KVH_API int kvh_paged_attention_static(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                               const void* k_cache, const int64_t k_cache_strides[3],
+                               const void* v_cache, const int64_t v_cache_strides[3],
+                               int64_t num_blocks,
+                               void* out, int64_t o_tok_stride, int64_t o_head_stride,
+                               const int64_t* block_tables, int64_t bt_row_stride, int32_t max_blocks_per_seq,
+                               const int64_t* seq_lens, const int64_t* query_start_loc,
+                               int64_t num_tokens, int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                               int32_t head_dim, int32_t block_size, int32_t max_query_len, float scale,
+                               int32_t dtype, void* stream);
 
 /*
  * kvh_paged_attention over E4M3 caches (see reshape_and_cache_fp8): keys and values are

@@ -91,6 +91,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _vp, _sz, _vp,  # workspace, stream
         ],  # fmt: skip
     ),
+    "kvh_paged_attention_static": (
+        ctypes.c_int,
+        [
+            _vp, _i64, _i64,  # q
+            _vp, _i64p, _vp, _i64p, _i64,  # caches, num_blocks
+            _vp, _i64, _i64,  # out
+            _vp, _i64, _i32,  # block tables
+            _vp, _vp,  # seq_lens, query_start_loc
+            _i64, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32,  # sizes, scale, dtype
+            _vp,  # stream
+        ],  # fmt: skip
+    ),
     "kvh_paged_attention_fp8": (
         ctypes.c_int,
         [

@@ -3,6 +3,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "kvhip.h"  // include/ is on the include path
 #include "kvh_device.h"
 #include "kvh_internal.h"
@@ -105,6 +108,9 @@ const char* kvh_strerror(int status) {
     case KVH_E_ALIGN: return "kvhip: pointer or stride not aligned (16-byte rows required)";
     case KVH_E_UNSUPPORTED: return "kvhip: unsupported head_dim / block_size / GQA combination";
     case KVH_E_WORKSPACE: return "kvhip: workspace missing or too small";
+    case KVH_E_SCRATCH:
+      return "kvhip: launch needs more workspace than the library's static scratch holds "
+             "(KVH_STATIC_SCRATCH_BYTES); use kvh_paged_attention with a workspace";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);
@@ -451,7 +457,68 @@ static int paged_attention_impl(const void* q, int64_t q_tok_stride, int64_t q_h
   return st;
 }
 
+// ---------------------------------------------------------------------------------------
+// Static scratch for kvh_paged_attention_static: the split-K workspace as a device array of
+// this library, so a caller that cannot allocate (HIP graph capture, serving loops that
+// forbid hipMalloc) passes only inputs and outputs. Each device holds its own copy for the
+// life of the process. In host code `g_static_scratch` is only the host-side handle of the
+// array: its device address comes from hipGetSymbolAddress, once per device, with that
+// device current, and only that address is ever handed to kernels.
+static __device__ __align__(256) unsigned char g_static_scratch[KVH_STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch (resolved on its first use there).
+int static_scratch_address(void** addr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return KVH_E_UNSUPPORTED;
+  void* a = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!a) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    a = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!a) {
+      e = hipGetSymbolAddress(&a, HIP_SYMBOL(g_static_scratch));
+      if (e != hipSuccess) return (int)e;
+      if (!a) return (int)hipErrorInvalidSymbol;
+      g_scratch_addr[dev].store(a, std::memory_order_release);
+    }
+  }
+  *addr = a;
+  return KVH_OK;
+}
+}  // namespace
+
 extern "C" {
+
+int kvh_paged_attention_static(const void* q, int64_t q_tok_stride, int64_t q_head_stride, const void* k_cache,
+                               const int64_t k_cache_strides[3], const void* v_cache,
+                               const int64_t v_cache_strides[3], int64_t num_blocks, void* out,
+                               int64_t o_tok_stride, int64_t o_head_stride, const int64_t* block_tables,
+                               int64_t bt_row_stride, int32_t max_blocks_per_seq, const int64_t* seq_lens,
+                               const int64_t* query_start_loc, int64_t num_tokens, int32_t num_seqs,
+                               int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                               int32_t max_query_len, float scale, int32_t dtype, void* stream) {
+  int st = check_attention_shape(num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
+                                 block_size, dtype);
+  if (st != KVH_OK) return st;
+  if (num_tokens == 0 || num_seqs == 0) return KVH_OK;
+  const size_t need = make_plan(num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
+                                block_size, max_query_len, dtype)
+                          .ws_bytes;
+  if (need > (size_t)KVH_STATIC_SCRATCH_BYTES) return KVH_E_SCRATCH;
+  void* ws = nullptr;
+  if (need > 0 && (st = static_scratch_address(&ws)) != KVH_OK) return st;
+  return paged_attention_impl(q, q_tok_stride, q_head_stride, k_cache, k_cache_strides, v_cache, v_cache_strides,
+                              num_blocks, out, o_tok_stride, o_head_stride, block_tables, bt_row_stride,
+                              max_blocks_per_seq, seq_lens, query_start_loc, num_tokens, num_seqs, num_heads,
+                              num_kv_heads, head_dim, block_size, max_query_len, scale, dtype, false, 1.f, 1.f, ws,
+                              need > 0 ? (size_t)KVH_STATIC_SCRATCH_BYTES : 0, stream);
+}
 
 int kvh_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride, const void* k_cache,
                         const int64_t k_cache_strides[3], const void* v_cache, const int64_t v_cache_strides[3],

@@ -13,7 +13,7 @@ from kvserve_amd import _lib, attention, workloads
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "kvhip.h"
 
-E_NULL, E_SHAPE, E_DTYPE, E_ALIGN, E_UNSUPPORTED, E_WORKSPACE = -1, -2, -3, -4, -5, -6
+E_NULL, E_SHAPE, E_DTYPE, E_ALIGN, E_UNSUPPORTED, E_WORKSPACE, E_SCRATCH = -1, -2, -3, -4, -5, -6, -7
 
 
 @pytest.fixture(scope="module")
@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_strerror_covers_every_status(lib):
-    for code in (0, E_NULL, E_SHAPE, E_DTYPE, E_ALIGN, E_UNSUPPORTED, E_WORKSPACE):
+    for code in (0, E_NULL, E_SHAPE, E_DTYPE, E_ALIGN, E_UNSUPPORTED, E_WORKSPACE, E_SCRATCH):
         msg = lib.kvh_strerror(code).decode()
         assert msg and (code == 0 or "kvhip" in msg)
     assert lib.kvh_strerror(-99).decode() == "kvhip: unknown status"
@@ -105,6 +105,24 @@ def test_cache_write_validation(lib):
     bad = list(args)
     bad[0] = 0x1001
     assert f(*bad, 2, None) == E_ALIGN
+
+
+def test_static_entry_rejects_oversized_launch_on_the_host(lib):
+    """kvh_paged_attention_static checks its workspace need against the static scratch
+    (256 MiB) before touching the device: no GPU is needed to see the rejection."""
+    a = _attn_args(T=2500, B=2004, W=280, bt_rs=280, max_q=384)
+    f = lib.kvh_paged_attention_static
+    args = (a["q"], a["q_ts"], a["q_hs"], a["kc"], _lib.i64x3(a["kcs"]), a["vc"], _lib.i64x3(a["vcs"]), a["nb"],
+            a["out"], a["o_ts"], a["o_hs"], a["bt"], a["bt_rs"], a["W"], a["sl"], a["qsl"], a["T"], a["B"], a["H"],
+            a["Hkv"], a["D"], a["BS"], a["max_q"], a["scale"], a["dtype"], None)  # fmt: skip
+    assert lib.kvh_paged_attention_workspace_size(2500, 2004, 32, 8, 128, 280, 16, 384, 2) > 256 << 20
+    assert f(*args) == E_SCRATCH
+    bad = list(args)
+    bad[18] = 30  # H % Hkv != 0: the shape check comes first
+    assert f(*bad) == E_SHAPE
+    bad = list(args)
+    bad[16] = 0  # no tokens: nothing to launch
+    assert f(*bad) == 0
 
 
 def test_workspace_follows_the_plan(lib):
