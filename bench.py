@@ -254,8 +254,8 @@ def measure_engine(name: str, batches: list[int], prompt_len: int = 512, steps: 
     max_len = prompt_len + steps + 16
     model = build_model(cfg, "cuda:0", torch.bfloat16, max_len, backend=HipAttention, seed=seed)
     blocks = max(batches) * -(-max_len // 16) + 16
-    runner = ModelRunner(model, num_blocks=blocks, block_size=16, max_model_len=max_len, use_graphs=True,
-                         max_graph_batch=max(batches))  # fmt: skip
+    runner = ModelRunner(model, num_blocks=blocks, block_size=16, max_model_len=max_len, decode_graphs=True,
+                         piecewise_graphs=False, max_graph_batch=max(batches))  # fmt: skip
     out = {}
     for b in batches:
         seqs = [Sequence([1000 + (i * 7 + j) % 30000 for j in range(prompt_len)]) for i in range(b)]

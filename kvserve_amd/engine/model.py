@@ -1,323 +1,304 @@
-"""Llama decoder over a flat, paged-KV batch, calling an attention backend.
+"""Paged Llama decoder used to drive the attention backend as kvserve's model drives it.
 
-The layer structure is the reference's (src/kvserve/model.py): tokens of all sequences
-packed without padding, fused QKV and gate/up projections, K/V written to and read from
-the shared paged pool through `backend.write_kv` / `backend.forward`, and the forward pass
-split at the attention calls into num_layers + 1 row-wise pieces (model.py:187-212).
-GEMMs, norms and RoPE are PyTorch (hipBLASLt GEMMs on ROCm); attention is the backend's. On
-the GPU with 16-bit weights (`fused_ops`), the residual add + RMSNorm and SiLU * up run as
-single libkvhip kernels and projections of at most 4 rows as its GEMV, the gate_up one with
-SiLU * up in its epilogue (engine/ops.py).
+Layout of the computation. A step's tokens (every sequence's, packed without padding) flow
+through `num_layers + 1` *stages* separated by `num_layers` *attention steps*:
+
+    stage 0        embed -> norm -> fused QKV projection of layer 0
+    attention i    RoPE(q, k), K/V into the paged cache, paged attention       (backend)
+    stage i + 1    o_proj -> residual -> norm -> gate_up -> SiLU * up -> down -> residual
+                   -> norm -> fused QKV projection of layer i + 1  (final norm for the last)
+
+Stages are row-wise over the flat batch and never touch the KV cache, so they can be
+replayed from HIP graphs captured at a padded token count while the attention steps run on
+the real tokens with the step's own metadata (kvserve's piecewise boundary,
+src/kvserve/cuda_graph.py:140-241). Ending a stage at the *unrotated* projection puts RoPE
+on the attention side of the boundary, where the HIP backend applies it in the same kernel
+that writes the cache (`HipAttention.rope_and_cache`); backends without that kernel get the
+split + RoPE + `write_kv` sequence of the reference's `Attention.project` / `attend`
+(src/kvserve/model.py:84-108).
+
+Weights are plain tensors per layer (`LayerWeights`), the projections fused as the
+reference fuses them (q|k|v rows, gate|up rows). The arithmetic is Hugging Face Llama's
+(RMSNorm with fp32 statistics, rotate-half RoPE with Llama 3 frequency scaling, SiLU MLP),
+which the CPU tests pin against transformers' own model. On the GPU with 16-bit weights the
+row-wise work runs on libkvhip's layer kernels (`engine.ops`).
 """
 
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass, field
 from pathlib import Path
+from typing import NamedTuple
 
 import torch
 import torch.nn.functional as F
-from torch import nn
 
 from kvserve_amd.attention import AttentionMetadata, HipAttention
 from kvserve_amd.engine import ops
 from kvserve_amd.engine.config import ModelConfig
 
+# -- arithmetic ------------------------------------------------------------------------------
 
-class RMSNorm(nn.Module):
-    """x / rms(x) in fp32, cast back, times the weight (model.py:22-32)."""
 
-    def __init__(self, dim: int, eps: float):
-        super().__init__()
-        self.weight = nn.Parameter(torch.ones(dim))
-        self.eps = eps
-
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        x32 = x.float()
-        x32 = x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + self.eps)
-        return self.weight * x32.to(x.dtype)
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """weight * (x / sqrt(mean(x^2) + eps)), statistics in fp32, normalised rows rounded to
+    x's dtype before the weight multiplies them (Llama's RMSNorm; reference model.py:22-32)."""
+    xf = x.float()
+    inv_rms = torch.rsqrt(xf.square().mean(dim=-1, keepdim=True) + eps)
+    return weight * (xf * inv_rms).to(x.dtype)
 
 
 def rope_inv_freq(cfg: ModelConfig) -> torch.Tensor:
-    """Inverse frequencies, with Llama 3's frequency-dependent long-context scaling when the
-    config asks for it (model.py:35-52): wavelengths above original_ctx / low_freq_factor are
-    divided by `factor`, those below original_ctx / high_freq_factor kept, and the band in
-    between interpolated linearly in original_ctx / wavelength."""
-    d = cfg.head_dim
-    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.int64).float() / d))
+    """RoPE inverse frequencies theta^(-2i/D), i < D/2, with Llama 3's long-context rescaling
+    when the config carries it (reference model.py:35-52): a component whose wavelength
+    2 pi / f exceeds original_ctx / low_freq_factor is slowed by `factor`, one below
+    original_ctx / high_freq_factor is kept, and in between the two are blended linearly in
+    original_ctx / wavelength."""
+    half = torch.arange(0, cfg.head_dim, 2, dtype=torch.int64).float()
+    base = 1.0 / (cfg.rope_theta ** (half / cfg.head_dim))
     sc = cfg.rope_scaling or {}
     if sc.get("rope_type", sc.get("type")) != "llama3":
-        return inv
-    factor, lo, hi = sc["factor"], sc["low_freq_factor"], sc["high_freq_factor"]
+        return base
     ctx = sc["original_max_position_embeddings"]
-    wavelen = 2 * math.pi / inv
-    long_wave = wavelen > ctx / lo
-    short_wave = wavelen < ctx / hi
-    blend = (ctx / wavelen - lo) / (hi - lo)
-    mid = (1 - blend) * inv / factor + blend * inv
-    return torch.where(long_wave, inv / factor, torch.where(short_wave, inv, mid))
+    lo, hi, factor = sc["low_freq_factor"], sc["high_freq_factor"], sc["factor"]
+    wavelength = 2 * math.pi / base
+    t = (ctx / wavelength - lo) / (hi - lo)  # 0 at the long-wave edge, 1 at the short-wave edge
+    blended = (1 - t) * base / factor + t * base
+    out = torch.where(wavelength < ctx / hi, base, blended)
+    return torch.where(wavelength > ctx / lo, base / factor, out)
 
 
-class RotaryEmbedding(nn.Module):
-    """cos/sin tables for positions [0, max_positions), fp32; rotate-half convention."""
-
-    def __init__(self, cfg: ModelConfig, max_positions: int, device=None):
-        super().__init__()
-        freqs = torch.outer(torch.arange(max_positions, dtype=torch.float32), rope_inv_freq(cfg))
-        emb = torch.cat([freqs, freqs], dim=-1)
-        self.register_buffer("cos", emb.cos().to(device), persistent=False)
-        self.register_buffer("sin", emb.sin().to(device), persistent=False)
-
-    def forward(self, q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor):
-        cos = self.cos[positions].to(q.dtype)[:, None]  # [T, 1, D]
-        sin = self.sin[positions].to(q.dtype)[:, None]
-        return q * cos + _rotate_half(q) * sin, k * cos + _rotate_half(k) * sin
+def rope_tables(cfg: ModelConfig, max_positions: int, device=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 cos / sin tables [max_positions, head_dim]: angle p * f_i in both halves of a row."""
+    angles = torch.arange(max_positions, dtype=torch.float32)[:, None] * rope_inv_freq(cfg)[None, :]
+    angles = angles.repeat(1, 2)
+    return angles.cos().to(device), angles.sin().to(device)
 
 
-def _rotate_half(x: torch.Tensor) -> torch.Tensor:
-    a, b = x.chunk(2, dim=-1)
-    return torch.cat([-b, a], dim=-1)
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x [T, heads, D] rotated by per-token cos / sin rows [T, D] (already in x's dtype):
+    x * cos + (-x2, x1) * sin with x1, x2 the two halves of the last dim."""
+    d = x.shape[-1] // 2
+    turned = torch.cat((-x[..., d:], x[..., :d]), dim=-1)
+    return x * cos[:, None, :] + turned * sin[:, None, :]
 
 
-class Attention(nn.Module):
-    def __init__(self, cfg: ModelConfig, backend):
-        super().__init__()
-        self.backend = backend
-        self.num_heads, self.num_kv_heads, self.head_dim = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
-        self.q_size = cfg.num_heads * cfg.head_dim
-        self.kv_size = cfg.num_kv_heads * cfg.head_dim
-        self.qkv_proj = nn.Linear(cfg.hidden_size, self.q_size + 2 * self.kv_size, bias=False)
-        self.o_proj = nn.Linear(self.q_size, cfg.hidden_size, bias=False)
-        self.scale = self.head_dim**-0.5
-        # per-layer scales of a float8_e4m3fn KV cache (unused for 16-bit caches)
-        self.k_scale = self.v_scale = 1.0
-
-    def _kv_scales(self, cache: torch.Tensor) -> dict:
-        return {"k_scale": self.k_scale, "v_scale": self.v_scale} if cache.dtype == torch.float8_e4m3fn else {}
-
-    def project(self, x: torch.Tensor, positions: torch.Tensor, rope: RotaryEmbedding):
-        """[T, hidden] -> q [T, H, D], k [T, Hkv, D] (RoPE applied), v [T, Hkv, D] (a strided
-        view of the fused projection, as in model.py:84-94)."""
-        n = x.shape[0]
-        q, k, v = self.qkv_proj(x).split([self.q_size, self.kv_size, self.kv_size], dim=-1)
-        q = q.view(n, self.num_heads, self.head_dim)
-        k = k.view(n, self.num_kv_heads, self.head_dim)
-        v = v.view(n, self.num_kv_heads, self.head_dim)
-        q, k = rope(q, k, positions)
-        return q, k, v
-
-    def attend(self, q, k, v, kv_cache: torch.Tensor, meta: AttentionMetadata, out: torch.Tensor | None = None):
-        """Write this step's K/V into the paged cache and attend over it (model.py:96-108)."""
-        k_cache, v_cache = kv_cache[0], kv_cache[1]
-        sc = self._kv_scales(k_cache)
-        self.backend.write_kv(k_cache, v_cache, k, v, meta.slot_mapping, **sc)
-        return self.backend.forward(q, k_cache, v_cache, meta, self.scale, out=out, **sc)
-
-    def attend_fused(self, qkv, positions, rope: RotaryEmbedding, kv_cache: torch.Tensor, meta: AttentionMetadata,
-                     out: torch.Tensor | None = None, h: torch.Tensor | None = None):  # fmt: skip
-        """RoPE, QKV split and the cache write in the backend's one kernel, then attention: the
-        same result as project() + attend() (bit for bit) with the RoPE moved out of the piece.
-        With qkv None the piece stopped before the projection (h, decode-sized batches): the
-        backend's gemv_rope_and_cache projects and rotates in the same kernel."""
-        k_cache, v_cache = kv_cache[0], kv_cache[1]
-        sc = self._kv_scales(k_cache)
-        if qkv is None:
-            q = self.backend.gemv_rope_and_cache(h, self.qkv_proj.weight, positions, rope.cos, rope.sin, k_cache,
-                                                 v_cache, meta.slot_mapping, self.num_heads, **sc)  # fmt: skip
-        else:
-            q = self.backend.rope_and_cache(qkv, positions, rope.cos, rope.sin, k_cache, v_cache, meta.slot_mapping,
-                                            self.num_heads, **sc)  # fmt: skip
-        return self.backend.forward(q, k_cache, v_cache, meta, self.scale, out=out, **sc)
+# -- weights ---------------------------------------------------------------------------------
 
 
-class MLP(nn.Module):
-    def __init__(self, cfg: ModelConfig):
-        super().__init__()
-        self.gate_up_proj = nn.Linear(cfg.hidden_size, 2 * cfg.intermediate_size, bias=False)
-        self.down_proj = nn.Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
-
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        gate, up = self.gate_up_proj(x).chunk(2, dim=-1)
-        return self.down_proj(F.silu(gate) * up)
-
-
-class DecoderLayer(nn.Module):
-    def __init__(self, cfg: ModelConfig, backend):
-        super().__init__()
-        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
-        self.self_attn = Attention(cfg, backend)
-        self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
-        self.mlp = MLP(cfg)
+@dataclass
+class LayerWeights:
+    attn_norm: torch.Tensor  # [hidden]
+    wqkv: torch.Tensor  # [(H + 2 Hkv) D, hidden]: query heads, then key heads, then value heads
+    wo: torch.Tensor  # [hidden, H D]
+    mlp_norm: torch.Tensor  # [hidden]
+    w_gate_up: torch.Tensor  # [2 I, hidden]: gate rows, then up rows
+    w_down: torch.Tensor  # [hidden, I]
+    k_scale: float = 1.0  # per-layer scales of a float8_e4m3fn KV cache
+    v_scale: float = 1.0
 
 
-# Hugging Face projection name -> (fused parameter, shard)
-_FUSED = {
-    "q_proj": ("qkv_proj", 0),
-    "k_proj": ("qkv_proj", 1),
-    "v_proj": ("qkv_proj", 2),
-    "gate_proj": ("gate_up_proj", 0),
-    "up_proj": ("gate_up_proj", 1),
-}
+@dataclass
+class Weights:
+    embed: torch.Tensor  # [vocab, hidden]
+    layers: list[LayerWeights] = field(default_factory=list)
+    final_norm: torch.Tensor | None = None
+    lm_head: torch.Tensor | None = None  # the embedding itself when tied
 
 
-class LlamaForCausalLM(nn.Module):
-    def __init__(self, cfg: ModelConfig, max_positions: int, backend=HipAttention):
-        super().__init__()
+def random_weights(cfg: ModelConfig, device, dtype: torch.dtype, seed: int = 0, std: float = 0.02) -> Weights:
+    """Synthetic weights of the model's shape: N(0, std) matrices drawn on `device` from one
+    seeded generator (in a fixed order), norm weights 1."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+
+    def normal(*shape: int) -> torch.Tensor:
+        return (torch.randn(shape, generator=gen, device=device, dtype=torch.float32) * std).to(dtype)
+
+    def ones() -> torch.Tensor:
+        return torch.ones(cfg.hidden_size, device=device, dtype=dtype)
+
+    H, Hkv, D, hid, inter = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.hidden_size, cfg.intermediate_size
+    w = Weights(embed=normal(cfg.vocab_size, hid))
+    for _ in range(cfg.num_layers):
+        w.layers.append(LayerWeights(ones(), normal((H + 2 * Hkv) * D, hid), normal(hid, H * D), ones(),
+                                     normal(2 * inter, hid), normal(hid, inter)))  # fmt: skip
+    w.final_norm = ones()
+    w.lm_head = w.embed if cfg.tie_word_embeddings else normal(cfg.vocab_size, hid)
+    return w
+
+
+def load_hf_weights(path: Path, cfg: ModelConfig, device, dtype: torch.dtype) -> Weights:
+    """Weights from a Hugging Face Llama checkpoint (*.safetensors under `path`), with the
+    separate q/k/v and gate/up matrices concatenated row-wise into the fused projections."""
+    from safetensors import safe_open
+
+    files = sorted(Path(path).glob("*.safetensors"))
+    where: dict[str, Path] = {}
+    for f in files:
+        with safe_open(str(f), framework="pt") as h:
+            for name in h.keys():  # noqa: SIM118  (a safetensors handle, not a mapping)
+                where[name] = f
+
+    def get(name: str) -> torch.Tensor:
+        for key in (name, f"model.{name}"):
+            if key in where:
+                with safe_open(str(where[key]), framework="pt") as h:
+                    return h.get_tensor(key).to(device=device, dtype=dtype)
+        raise KeyError(f"{path}: checkpoint has no tensor {name!r}")
+
+    w = Weights(embed=get("embed_tokens.weight"))
+    for i in range(cfg.num_layers):
+        p = f"layers.{i}."
+        qkv = torch.cat([get(p + f"self_attn.{x}_proj.weight") for x in "qkv"])
+        gate_up = torch.cat([get(p + "mlp.gate_proj.weight"), get(p + "mlp.up_proj.weight")])
+        w.layers.append(LayerWeights(get(p + "input_layernorm.weight"), qkv, get(p + "self_attn.o_proj.weight"),
+                                     get(p + "post_attention_layernorm.weight"), gate_up,
+                                     get(p + "mlp.down_proj.weight")))  # fmt: skip
+    w.final_norm = get("norm.weight")
+    w.lm_head = w.embed if cfg.tie_word_embeddings else get("lm_head.weight")
+    return w
+
+
+# -- the model -------------------------------------------------------------------------------
+
+
+class StageOut(NamedTuple):
+    """What a stage hands to the next attention step (or, after the last stage, the final
+    hidden states in `resid`). Exactly one of `qkv` / `normed` is set before an attention step:
+    `normed` when the projection is deferred into the attention step's fused kernel."""
+
+    resid: torch.Tensor  # [T, hidden] residual stream
+    qkv: torch.Tensor | None  # [T, (H + 2 Hkv) D] fused projection, not yet rotated
+    normed: torch.Tensor | None  # [T, hidden] the layer's normalised input
+
+
+class PagedLlama:
+    """A Llama decoder over the flat paged batch, calling an attention backend with kvserve's
+    interface (`write_kv` / `forward`, src/kvserve/attention.py:39-102)."""
+
+    def __init__(self, cfg: ModelConfig, weights: Weights, backend=HipAttention, max_positions: int = 4096,
+                 fused_ops: bool | None = None):  # fmt: skip
         self.cfg = cfg
-        self.max_positions = max_positions
-        self.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_size)
-        self.layers = nn.ModuleList(DecoderLayer(cfg, backend) for _ in range(cfg.num_layers))
-        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
-        self.lm_head = nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
-        if cfg.tie_word_embeddings:
-            self.lm_head.weight = self.embed_tokens.weight
-        self.rope = RotaryEmbedding(cfg, max_positions)
-        # a backend with a fused RoPE + cache-write kernel takes the raw QKV projection
-        self.fused_rope = bool(getattr(backend, "fused_rope_cache", False))
+        self.w = weights
         self.backend = backend
-        # decode-sized batches: the QKV projection fused with RoPE + cache write (fused_ops only)
-        self._gemv_rope = hasattr(backend, "gemv_rope_and_cache")
-        # libkvhip's fused elementwise kernels and GEMV (set on the GPU, 16-bit weights)
-        self.fused_ops = False
+        self.device, self.dtype = weights.embed.device, weights.embed.dtype
+        self.max_positions = max_positions
+        self.cos, self.sin = rope_tables(cfg, max_positions, self.device)
+        self.scale = cfg.head_dim**-0.5
+        self.q_width = cfg.num_heads * cfg.head_dim
+        self.kv_width = cfg.num_kv_heads * cfg.head_dim
+        # what the backend offers beyond write_kv / forward
+        self.fused_rope = callable(getattr(backend, "rope_and_cache", None))
+        self.fused_projection = callable(getattr(backend, "gemv_rope_and_cache", None))
+        probe = torch.empty(0, dtype=self.dtype, device=self.device)
+        self.fused_ops = ops.enabled(probe) if fused_ops is None else bool(fused_ops)
+        if self.fused_ops and not ops.enabled(probe):
+            raise ValueError("libkvhip layer kernels need a GPU and fp16 / bf16 weights")
 
-    @torch.inference_mode()
-    def forward(self, input_ids: torch.Tensor, positions: torch.Tensor, kv_caches: torch.Tensor,
-                meta: AttentionMetadata) -> torch.Tensor:  # fmt: skip
-        """Final hidden states [T, hidden]; kv_caches [layers, 2, blocks, block_size, kv_heads, D]."""
-        x, q, k, v = self.piece(0, input_ids, positions, None, None)
-        for i, layer in enumerate(self.layers):
-            if self.fused_rope:
-                attn = layer.self_attn.attend_fused(q, positions, self.rope, kv_caches[i], meta, h=k)
-            else:
-                attn = layer.self_attn.attend(q, k, v, kv_caches[i], meta)
-            x, q, k, v = self.piece(i + 1, input_ids, positions, x, attn)
-        return x
+    @property
+    def num_layers(self) -> int:
+        return len(self.w.layers)
 
-    def piece(self, i: int, input_ids, positions, x, attn):
-        """Everything between attention call i - 1 and attention call i (i = 0 .. num_layers):
-        finish layer i - 1 (output projection, residual, MLP), start layer i (norm, QKV, RoPE).
-        Row-wise, never touches the KV cache (model.py:187-212). Returns (x, q, k, v), or
-        (final hidden states, None, None, None) for the last piece. With a fused-RoPE backend
-        the piece stops at the QKV projection: (x, qkv, None, None)."""
+    # -- row-wise stages ------------------------------------------------------------------------
+    def _linear(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        return ops.linear(x, w) if self.fused_ops else F.linear(x, w)
+
+    def _add_norm(self, x: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tensor):
+        """(x + delta, RMSNorm(x + delta)); delta None: (x, RMSNorm(x))."""
+        eps = self.cfg.rms_norm_eps
         if self.fused_ops:
-            return self._piece_fused(i, input_ids, positions, x, attn)
-        if i == 0:
-            x = self.embed_tokens(input_ids)
-        else:
-            prev = self.layers[i - 1]
-            x = x + prev.self_attn.o_proj(attn.flatten(1))
-            x = x + prev.mlp(prev.post_attention_layernorm(x))
-        if i == len(self.layers):
-            return self.norm(x), None, None, None
-        layer = self.layers[i]
-        h = layer.input_layernorm(x)
-        if self.fused_rope:
-            return x, layer.self_attn.qkv_proj(h), None, None
-        q, k, v = layer.self_attn.project(h, positions, self.rope)
-        return x, q, k, v
+            return ops.add_rmsnorm(x, delta, weight, eps)
+        if delta is not None:
+            x = x + delta
+        return x, rms_norm(x, weight, eps)
 
-    def _piece_fused(self, i: int, input_ids, positions, x, attn):
-        """piece() with libkvhip's kernels: the same operations, the residual adds fused into
-        the following norm, SiLU * up in one pass and small-batch projections on the GEMV."""
-        n = len(self.layers)
-        if i == 0:
-            x, h = ops.add_rmsnorm(self.embed_tokens(input_ids), None, self.layers[0].input_layernorm.weight,
-                                   self.layers[0].input_layernorm.eps)  # fmt: skip
-        else:
-            prev = self.layers[i - 1]
-            o = ops.linear(attn.flatten(1), prev.self_attn.o_proj.weight)
-            x, h = ops.add_rmsnorm(x, o, prev.post_attention_layernorm.weight, prev.post_attention_layernorm.eps)
-            d = ops.linear(ops.mlp_act(h, prev.mlp.gate_up_proj.weight), prev.mlp.down_proj.weight)
-            norm = self.norm if i == n else self.layers[i].input_layernorm
-            x, h = ops.add_rmsnorm(x, d, norm.weight, norm.eps)
-            if i == n:
-                return h, None, None, None
-        layer = self.layers[i]
-        if self.fused_rope and self._gemv_rope and ops.qkv_rope_fused(h.shape[0], *layer.self_attn.qkv_proj.weight.shape):
-            return x, None, h, None  # the projection runs in the attention step (gemv_rope_and_cache)
-        qkv = ops.linear(h, layer.self_attn.qkv_proj.weight)
-        if self.fused_rope:
-            return x, qkv, None, None
-        q, k, v = qkv.split([layer.self_attn.q_size, layer.self_attn.kv_size, layer.self_attn.kv_size], dim=-1)
-        q = q.view(-1, layer.self_attn.num_heads, layer.self_attn.head_dim)
-        k = k.view(-1, layer.self_attn.num_kv_heads, layer.self_attn.head_dim)
-        v = v.view(-1, layer.self_attn.num_kv_heads, layer.self_attn.head_dim)
-        q, k = self.rope(q, k, positions)
-        return x, q, k, v
-
-    @torch.inference_mode()
-    def compute_logits(self, hidden: torch.Tensor) -> torch.Tensor:
+    def _mlp(self, h: torch.Tensor, lw: LayerWeights) -> torch.Tensor:
         if self.fused_ops:
-            return ops.linear(hidden, self.lm_head.weight).float()
-        return self.lm_head(hidden).float()
+            return ops.linear(ops.mlp_act(h, lw.w_gate_up), lw.w_down)
+        gate, up = F.linear(h, lw.w_gate_up).chunk(2, dim=-1)
+        return F.linear(F.silu(gate) * up, lw.w_down)
 
-    # -- weights ----------------------------------------------------------------------------
-    def _shard_range(self, target: str, shard: int) -> tuple[int, int]:
-        c = self.cfg
-        if target == "qkv_proj":
-            q, kv = c.num_heads * c.head_dim, c.num_kv_heads * c.head_dim
-            return [(0, q), (q, kv), (q + kv, kv)][shard]
-        return shard * c.intermediate_size, c.intermediate_size
+    def defers_projection(self, rows: int) -> bool:
+        """Whether a layer's QKV projection over `rows` rows moves into the attention step
+        (the backend's projection + RoPE + cache-write kernel, decode-sized batches only)."""
+        if not (self.fused_ops and self.fused_rope and self.fused_projection):
+            return False
+        return ops.qkv_rope_fused(rows, *self.w.layers[0].wqkv.shape)
+
+    def stage(self, i: int, input_ids: torch.Tensor | None, resid: torch.Tensor | None, attn: torch.Tensor | None,
+              defer: bool = False) -> StageOut:  # fmt: skip
+        """Stage i of num_layers + 1 (see the module docstring). Stage 0 reads `input_ids`; a
+        later stage reads the residual stream and layer i - 1's attention output [T, H, D].
+        `defer` leaves the next projection to the attention step (`defers_projection`)."""
+        L = self.num_layers
+        if i == 0:
+            x, h = self._add_norm(F.embedding(input_ids, self.w.embed), None, self.w.layers[0].attn_norm)
+        else:
+            prev = self.w.layers[i - 1]
+            o = self._linear(attn.flatten(1), prev.wo)
+            x, h = self._add_norm(resid, o, prev.mlp_norm)
+            nxt = self.w.final_norm if i == L else self.w.layers[i].attn_norm
+            x, h = self._add_norm(x, self._mlp(h, prev), nxt)
+            if i == L:
+                return StageOut(h, None, None)
+        if defer:
+            return StageOut(x, None, h)
+        return StageOut(x, self._linear(h, self.w.layers[i].wqkv), None)
+
+    # -- attention steps -----------------------------------------------------------------------
+    def attention(self, i: int, s: StageOut, positions: torch.Tensor, kv_layer: torch.Tensor, meta: AttentionMetadata,
+                  out: torch.Tensor | None = None, q_out: torch.Tensor | None = None) -> torch.Tensor:  # fmt: skip
+        """Layer i's attention over the pool slice kv_layer [2, blocks, BS, Hkv, D]: RoPE, this
+        step's K/V into the cache at meta.slot_mapping, then paged attention -> [T, H, D] (into
+        `out` if given; `q_out` receives the rotated queries on the fused paths)."""
+        lw = self.w.layers[i]
+        k_cache, v_cache = kv_layer[0], kv_layer[1]
+        sc = {"k_scale": lw.k_scale, "v_scale": lw.v_scale} if k_cache.dtype == torch.float8_e4m3fn else {}
+        H = self.cfg.num_heads
+        b = self.backend
+        if s.normed is not None:
+            q = b.gemv_rope_and_cache(s.normed, lw.wqkv, positions, self.cos, self.sin, k_cache, v_cache,
+                                      meta.slot_mapping, H, out=q_out, **sc)  # fmt: skip
+        elif self.fused_rope:
+            q = b.rope_and_cache(s.qkv, positions, self.cos, self.sin, k_cache, v_cache, meta.slot_mapping, H,
+                                 out=q_out, **sc)  # fmt: skip
+        else:
+            n, D = s.qkv.shape[0], self.cfg.head_dim
+            q, k, v = s.qkv.split([self.q_width, self.kv_width, self.kv_width], dim=-1)
+            cos, sin = self.cos[positions].to(q.dtype), self.sin[positions].to(q.dtype)
+            q = apply_rope(q.view(n, H, D), cos, sin)
+            k = apply_rope(k.view(n, -1, D), cos, sin)
+            b.write_kv(k_cache, v_cache, k, v.view(n, -1, D), meta.slot_mapping, **sc)
+        return b.forward(q, k_cache, v_cache, meta, self.scale, out=out, **sc)
+
+    # -- whole passes ----------------------------------------------------------------------------
+    @torch.inference_mode()
+    def hidden_states(self, input_ids: torch.Tensor, positions: torch.Tensor, kv_caches: torch.Tensor,
+                      meta: AttentionMetadata) -> torch.Tensor:  # fmt: skip
+        """Final hidden states [T, hidden] of one step; kv_caches [L, 2, blocks, BS, Hkv, D]."""
+        defer = self.defers_projection(input_ids.shape[0])
+        s = self.stage(0, input_ids, None, None, defer)
+        for i in range(self.num_layers):
+            a = self.attention(i, s, positions, kv_caches[i], meta)
+            s = self.stage(i + 1, None, s.resid, a, defer)
+        return s.resid
+
+    __call__ = hidden_states
 
     @torch.inference_mode()
-    def load_weights(self, path: Path) -> None:
-        """Load Hugging Face safetensors (model.layers.N.self_attn.q_proj.weight, ...) into the
-        fused parameters."""
-        from safetensors import safe_open
-
-        params = dict(self.named_parameters())
-        loaded: set[str] = set()
-        for file in sorted(Path(path).glob("*.safetensors")):
-            with safe_open(str(file), framework="pt") as f:
-                for hf_name in f.keys():  # noqa: SIM118
-                    name = hf_name.removeprefix("model.")
-                    module, _, leaf = name.rpartition(".")
-                    parent, _, proj = module.rpartition(".")
-                    t = f.get_tensor(hf_name)
-                    if proj in _FUSED:
-                        target, shard = _FUSED[proj]
-                        name = f"{parent}.{target}.{leaf}"
-                        off, size = self._shard_range(target, shard)
-                        params[name].data[off : off + size].copy_(t)
-                    else:
-                        if name == "lm_head.weight" and self.cfg.tie_word_embeddings:
-                            continue
-                        params[name].data.copy_(t)
-                    loaded.add(name)
-        missing = set(params) - loaded - ({"lm_head.weight"} if self.cfg.tie_word_embeddings else set())
-        if missing:
-            raise ValueError(f"weights missing from checkpoint: {sorted(missing)[:5]}")
-
-    @torch.inference_mode()
-    def init_random(self, seed: int, std: float = 0.02) -> None:
-        """Synthetic weights in place (no checkpoint): N(0, std) projections and embeddings,
-        norm weights 1. Drawn on the parameters' own device so large models fill quickly."""
-        dev = next(self.parameters()).device
-        gen = torch.Generator(device=dev).manual_seed(seed)
-        for name, p in self.named_parameters():
-            if name.endswith("layernorm.weight") or name == "norm.weight":
-                p.fill_(1.0)
-            else:
-                p.copy_(torch.randn(p.shape, generator=gen, device=dev, dtype=torch.float32).to(p.dtype) * std)
+    def logits(self, hidden: torch.Tensor) -> torch.Tensor:
+        """fp32 logits [T, vocab]."""
+        return self._linear(hidden, self.w.lm_head).float()
 
 
 def build_model(cfg: ModelConfig, device, dtype: torch.dtype, max_positions: int, backend=HipAttention,
                 weights: Path | None = None, seed: int = 0, std: float = 0.02,
-                fused_ops: bool | None = None) -> LlamaForCausalLM:  # fmt: skip
-    """Model on `device` in `dtype`: weights from a safetensors directory, else synthetic.
-    fused_ops (default: on a GPU with 16-bit weights) selects libkvhip's layer kernels."""
-    with torch.device("meta"):
-        model = LlamaForCausalLM(cfg, max_positions, backend)
-    model = model.to(dtype).to_empty(device=device)  # never materialise fp32 weights
-    if cfg.tie_word_embeddings:
-        model.lm_head.weight = model.embed_tokens.weight
-    if weights is not None:
-        model.load_weights(weights)
-    else:
-        model.init_random(seed, std)
-    model.rope = RotaryEmbedding(cfg, max_positions, device=device)  # fp32 tables, after the cast
-    probe = torch.empty(0, dtype=dtype, device=device)
-    model.fused_ops = ops.enabled(probe) if fused_ops is None else bool(fused_ops)
-    if model.fused_ops and not ops.enabled(probe):
-        raise ValueError("fused_ops needs a GPU and fp16 / bf16 weights")
-    return model.eval()
+                fused_ops: bool | None = None) -> PagedLlama:  # fmt: skip
+    """A PagedLlama on `device` in `dtype`: weights from a Hugging Face safetensors directory,
+    else synthetic (`random_weights`). fused_ops (default: on a GPU with 16-bit weights) selects
+    libkvhip's layer kernels for the row-wise work."""
+    device = torch.device(device)
+    w = load_hf_weights(weights, cfg, device, dtype) if weights is not None else random_weights(cfg, device, dtype,
+                                                                                                 seed, std)  # fmt: skip
+    return PagedLlama(cfg, w, backend, max_positions, fused_ops)

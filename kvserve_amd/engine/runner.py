@@ -1,299 +1,499 @@
-"""KV pool, step execution and HIP-graph decode replay for the engine harness.
+"""KV pool, step execution and the two HIP-graph modes of the engine harness.
 
-Follows the reference's ModelRunner (src/kvserve/model_runner.py:19-156) and
-DecodeGraphRunner (src/kvserve/cuda_graph.py:28-137), without its scheduler: the caller
-hands in sequences and the runner lays out the flat token batch, the slots
-(kv_cache.py:155-169) and the metadata (model_runner.py:165-197), runs the model and
-picks greedy tokens.
+A step is a list of (sequence, tokens to compute). `ModelRunner.execute` lays the tokens out
+as one flat batch, builds the attention metadata (on the device from resident block tables,
+or on the host as the reference does) and runs the model one of three ways, chosen per step
+as kvserve's ModelRunner chooses (src/kvserve/model_runner.py:130-143):
 
-The pool is [layers, 2, num_blocks + 1, block_size, kv_heads, head_dim]; the extra block
-is scratch space for graph padding rows, outside what sequences are given.
+  decode_graph  every sequence computes one token and the batch fits a captured bucket: the
+                whole forward pass replays from one HIP graph over static buffers, the batch
+                padded with rows that write the pool's scratch block;
+  piecewise     any other step of at most `max_piecewise_tokens` tokens: the model's row-wise
+                stages replay from HIP graphs captured per token-count bucket, and the
+                attention steps run eagerly in between on the real tokens (the boundary of
+                src/kvserve/cuda_graph.py:140-241);
+  eager         larger steps, or graphs disabled.
+
+`Batcher` forms the steps (no scheduler here): sequences in flight first, then arrivals, under
+a token budget, so prefill chunks and decodes share steps as they do under kvserve's
+scheduler.
 """
 
 from __future__ import annotations
 
+from collections import Counter
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from kvserve_amd.attention import AttentionMetadata, build_metadata
+from kvserve_amd.engine.model import PagedLlama, StageOut
 from kvserve_amd.metadata import DeviceMetadata, MetaBuffers
 
 
-@dataclass
+def decode_buckets(max_batch: int) -> list[int]:
+    """Padded batch sizes with a captured decode graph: 1, 2, 4, 8, every 8 up to 64 (where the
+    small-batch projections' cost follows the row count closely), every 32 beyond; the
+    largest is max_batch itself."""
+    sizes = [s for s in (1, 2, 4, 8) if s < max_batch]
+    sizes += [s for s in range(16, min(max_batch, 64) + 1, 8) if s < max_batch]
+    sizes += list(range(96, max_batch, 32))
+    return sizes + [max_batch]
+
+
+def token_buckets(max_tokens: int) -> list[int]:
+    """Token counts with captured piecewise stages: 1, 2, 4, 8, 16, 32, 48 (launch-bound steps,
+    where padding is nearly free), then from 64 on steps of 1/4 of the bucket: every 16 up to
+    128, every 32 up to 256, every 64 up to 512, every 128 up to 1024, every 256 beyond, so
+    padding never adds more than a quarter of the row-wise work; the largest is max_tokens."""
+    sizes = [1, 2, 4, 8, 16, 32, 48]
+    sizes += list(range(64, 129, 16)) + list(range(160, 257, 32)) + list(range(320, 513, 64))
+    sizes += list(range(640, 1025, 128)) + list(range(1280, max_tokens, 256))
+    return sorted({s for s in sizes if s < max_tokens} | {max_tokens})
+
+
+def _bucket(sizes: list[int], n: int) -> int | None:
+    for s in sizes:
+        if s >= n:
+            return s
+    return None
+
+
+# -- KV pool -----------------------------------------------------------------------------------
+
+
+class KVPool:
+    """The paged KV cache of every layer, [L, 2, num_blocks + 1, BS, Hkv, D], and its free list.
+    Block `num_blocks` is scratch for graph padding rows and is never handed out."""
+
+    def __init__(self, model: PagedLlama, num_blocks: int, block_size: int, dtype: torch.dtype):
+        cfg = model.cfg
+        shape = (cfg.num_layers, 2, num_blocks + 1, block_size, cfg.num_kv_heads, cfg.head_dim)
+        if dtype == torch.float8_e4m3fn:  # zero bytes viewed as E4M3 (+0)
+            self.tensor = torch.zeros(shape, dtype=torch.uint8, device=model.device).view(dtype)
+        else:
+            self.tensor = torch.zeros(shape, dtype=dtype, device=model.device)
+        self.num_blocks, self.block_size = num_blocks, block_size
+        self.scratch_block = num_blocks
+        self._free = list(range(num_blocks))[::-1]  # a stack: low ids first
+
+    @staticmethod
+    def blocks_in(model: PagedLlama, gib: float, block_size: int, dtype: torch.dtype) -> int:
+        """Blocks that fit `gib` GiB: K and V of every layer for `block_size` tokens each
+        (the reference's sizing, model_runner.py:94-98)."""
+        cfg = model.cfg
+        per_block = 2 * cfg.num_layers * block_size * cfg.num_kv_heads * cfg.head_dim * dtype.itemsize
+        return max(1, int(gib * 2**30) // per_block)
+
+    @property
+    def free_blocks(self) -> int:
+        return len(self._free)
+
+    def take(self, n: int) -> list[int]:
+        if n > len(self._free):
+            raise RuntimeError(f"KV pool exhausted: {n} blocks wanted, {len(self._free)} free")
+        got = self._free[len(self._free) - n :][::-1]
+        del self._free[len(self._free) - n :]
+        return got
+
+    def give_back(self, blocks: list[int]) -> None:
+        self._free.extend(reversed(blocks))
+
+
+@dataclass(eq=False)
 class Sequence:
-    token_ids: list[int]
-    block_table: list[int] = field(default_factory=list)
-    num_computed: int = 0  # tokens whose K/V are in the pool
-    prompt_len: int = -1  # set from token_ids when left at -1
+    tokens: list[int]  # prompt, then generated tokens
+    max_new_tokens: int = 1 << 30
+    table: list[int] = field(default_factory=list)  # physical block ids
+    computed: int = 0  # tokens whose K/V are in the pool
+    prompt_len: int = -1
 
     def __post_init__(self) -> None:
         if self.prompt_len < 0:
-            self.prompt_len = len(self.token_ids)
+            self.prompt_len = len(self.tokens)
 
     @property
-    def num_tokens(self) -> int:
-        return len(self.token_ids)
+    def pending(self) -> int:
+        return len(self.tokens) - self.computed
+
+    @property
+    def generated(self) -> list[int]:
+        return self.tokens[self.prompt_len :]
+
+    @property
+    def finished(self) -> bool:
+        return len(self.tokens) - self.prompt_len >= self.max_new_tokens
 
 
-def capture_sizes(max_batch: int) -> list[int]:
-    """Decode-graph buckets: 1, 2, 4, 8, then every 16 (cuda_graph.py:28-33)."""
-    sizes = [s for s in (1, 2, 4, 8) if s <= max_batch]
-    sizes += list(range(16, max_batch + 1, 16))
-    if sizes[-1] != max_batch:
-        sizes.append(max_batch)
-    return sizes
+# -- graphs --------------------------------------------------------------------------------------
+
+
+class _GraphCapture:
+    """Captures Python callables as HIP graphs on one shared memory pool (the first capture
+    creates it), after warm-up runs on a side stream so that lazy initialisation inside
+    libraries and allocator growth happen outside the capture."""
+
+    def __init__(self) -> None:
+        self.pool = None
+        self.side = torch.cuda.Stream()
+
+    def __call__(self, fn, warmups: int = 2):
+        main = torch.cuda.current_stream()
+        self.side.wait_stream(main)
+        with torch.cuda.stream(self.side):
+            for _ in range(warmups):
+                fn()
+        main.wait_stream(self.side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, pool=self.pool):
+            out = fn()
+        if self.pool is None:
+            self.pool = graph.pool()
+        return graph, out
 
 
 class DecodeGraphRunner:
-    """One HIP graph per padded decode batch size, replayed on static input buffers.
+    """Whole-forward HIP graphs for uniform decode steps, one per bucket of decode_buckets.
 
-    Padding rows write their K/V to the scratch block's first slot, read a one-token
-    context from the scratch block and are dropped from the output. The attention call
-    inside the graph never reads max_seq_len (the graph's metadata carries 1), and only the
-    first ceil(seq_len / block_size) table columns of a row are refreshed per step
-    (cuda_graph.py:111-137).
-    """
+    Static inputs (ids, positions, slots, tables, lengths) live in a MetaBuffers; a batch of n
+    replays the smallest bucket >= n, its rows n.. padded with token 0 at position 0, one key,
+    the scratch block's first slot and a table row of the scratch block, so they never touch
+    blocks a sequence owns. A refresh writes only the first `width` table columns (the longest
+    table of the batch): the kernels read ceil(seq_len / BS) columns, never max_seq_len."""
 
-    def __init__(self, model, kv_caches: torch.Tensor, scratch_block: int, block_size: int, max_batch: int,
-                 max_blocks_per_seq: int):  # fmt: skip
+    def __init__(self, model: PagedLlama, pool: KVPool, max_batch: int, max_blocks_per_seq: int):
+        self.model, self.pool = model, pool
+        self.sizes = decode_buckets(max_batch)
+        self.scratch_slot = pool.scratch_block * pool.block_size
+        self.buf = MetaBuffers(model.device, self.sizes[-1], self.sizes[-1], max_blocks_per_seq,
+                               slot_fill=self.scratch_slot, table_fill=pool.scratch_block)  # fmt: skip
+        self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+
+    @property
+    def max_batch(self) -> int:
+        return self.sizes[-1]
+
+    def _meta(self, n: int) -> AttentionMetadata:
+        b = self.buf
+        return AttentionMetadata(b.slot_mapping[:n], b.block_tables[:n], b.seq_lens[:n], b.query_lens[:n],
+                                 b.query_start_loc[: n + 1], max_seq_len=1, max_query_len=1)  # fmt: skip
+
+    @torch.inference_mode()
+    def capture(self, cap: _GraphCapture) -> None:
+        """Largest bucket first, so the smaller graphs reuse its pool memory."""
+        b = self.buf
+        for n in sorted(self.sizes, reverse=True):
+            meta = self._meta(n)
+            self.graphs[n] = cap(lambda n=n, meta=meta: self.model(b.input_ids[:n], b.positions[:n],
+                                                                   self.pool.tensor, meta))  # fmt: skip
+
+    @torch.inference_mode()
+    def replay_host(self, ids: list[int], positions: list[int], slots: list[int], tables: list[list[int]],
+                    seq_lens: list[int]) -> torch.Tensor:  # fmt: skip
+        """Refresh the static buffers from host lists (the reference's path) and replay."""
+        n = len(ids)
+        size = _bucket(self.sizes, n)
+        width = max(len(t) for t in tables)
+        vec = np.empty((4, size), dtype=np.int64)
+        vec[0, :n], vec[0, n:] = ids, 0
+        vec[1, :n], vec[1, n:] = positions, 0
+        vec[2, :n], vec[2, n:] = slots, self.scratch_slot
+        vec[3, :n], vec[3, n:] = seq_lens, 1
+        rows = np.full((size, width), self.pool.scratch_block, dtype=np.int64)
+        for r, t in enumerate(tables):
+            rows[r, : len(t)] = t
+        dev = self.buf.input_ids.device
+        v = torch.from_numpy(vec).to(dev, non_blocking=True)
+        b = self.buf
+        for dst, row in ((b.input_ids, 0), (b.positions, 1), (b.slot_mapping, 2), (b.seq_lens, 3)):
+            dst[:size].copy_(v[row])
+        b.block_tables[:size, :width].copy_(torch.from_numpy(rows).to(dev, non_blocking=True))
+        graph, out = self.graphs[size]
+        graph.replay()
+        return out[:n]
+
+    @torch.inference_mode()
+    def replay_device(self, dm: DeviceMetadata, keyed: list[tuple[object, list[int]]], starts: list[int],
+                      ids: list[int]) -> torch.Tensor:  # fmt: skip
+        """Refresh the static buffers on the device from the resident tables, then replay."""
+        n = len(ids)
+        size = _bucket(self.sizes, n)
+        width = max(len(t) for _, t in keyed)
+        dm.build(keyed, starts, [1] * n, ids, buffers=self.buf, pad_seqs=size - n, pad_slot=self.scratch_slot,
+                 table_pad=self.pool.scratch_block, width=width)  # fmt: skip
+        graph, out = self.graphs[size]
+        graph.replay()
+        return out[:n]
+
+
+class PiecewiseGraphRunner:
+    """HIP graphs of the model's row-wise stages, one per (stage, token bucket); the attention
+    steps run eagerly between the replays on the real rows (src/kvserve/cuda_graph.py:140-241).
+
+    Stages read and write static buffers: token ids, the residual stream, the fused QKV
+    projection and the attention output. Rows past the step's token count hold stale but
+    finite values from earlier steps; they are computed and dropped, and never reach attention
+    or the cache."""
+
+    def __init__(self, model: PagedLlama, max_tokens: int, ids: torch.Tensor | None = None):
         self.model = model
-        self.kv_caches = kv_caches
-        self.scratch_block = scratch_block
-        self.scratch_slot = scratch_block * block_size
-        self.sizes = capture_sizes(max_batch)
-        self.max_batch = self.sizes[-1]
-        b = self.max_batch
-        # static inputs, filled as cuda_graph.py:54-62 fills them
-        self.buf = MetaBuffers(kv_caches.device, b, b, max_blocks_per_seq, slot_fill=self.scratch_slot,
-                               table_fill=scratch_block)  # fmt: skip
-        self.input_ids, self.positions = self.buf.input_ids, self.buf.positions
-        self.slot_mapping, self.block_tables = self.buf.slot_mapping, self.buf.block_tables
-        self.seq_lens, self.query_lens = self.buf.seq_lens, self.buf.query_lens
-        self.query_start_loc = self.buf.query_start_loc
-        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
-        self.outputs: dict[int, torch.Tensor] = {}
+        self.sizes = token_buckets(max_tokens)
+        t, cfg, dev, dt = self.sizes[-1], model.cfg, model.device, model.dtype
+        self.ids = ids[:t] if ids is not None else torch.zeros(t, dtype=torch.long, device=dev)
+        if self.ids.shape[0] < t:
+            raise ValueError("the shared token-id buffer is shorter than the largest bucket")
+        self.resid = torch.zeros(t, cfg.hidden_size, dtype=dt, device=dev)
+        self.qkv = torch.zeros(t, (cfg.num_heads + 2 * cfg.num_kv_heads) * cfg.head_dim, dtype=dt, device=dev)
+        self.attn = torch.zeros(t, cfg.num_heads, cfg.head_dim, dtype=dt, device=dev)
+        self.q = torch.zeros(t, cfg.num_heads, cfg.head_dim, dtype=dt, device=dev)  # rotated queries
+        self.graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}
 
-    def _metadata(self, n: int) -> AttentionMetadata:
-        return AttentionMetadata(
-            slot_mapping=self.slot_mapping[:n],
-            block_tables=self.block_tables[:n],
-            seq_lens=self.seq_lens[:n],
-            query_lens=self.query_lens[:n],
-            query_start_loc=self.query_start_loc[: n + 1],
-            max_seq_len=1,  # not read by the HIP backend
-            max_query_len=1,
-        )
+    @property
+    def max_tokens(self) -> int:
+        return self.sizes[-1]
+
+    def _stage(self, i: int, n: int) -> None:
+        s = self.model.stage(i, self.ids[:n], self.resid[:n], self.attn[:n], defer=False)
+        self.resid[:n].copy_(s.resid)  # after the last stage: the final hidden states
+        if s.qkv is not None:
+            self.qkv[:n].copy_(s.qkv)
 
     @torch.inference_mode()
-    def capture(self) -> None:
-        """All buckets, largest first, sharing one memory pool; warm-up runs on a side stream
-        touch only the scratch block."""
-        pool = None
-        side = torch.cuda.Stream()
-        for n in reversed(self.sizes):
-            args = (self.input_ids[:n], self.positions[:n], self.kv_caches, self._metadata(n))
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                for _ in range(2):
-                    self.model(*args)
-            torch.cuda.current_stream().wait_stream(side)
-            torch.cuda.synchronize()
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, pool=pool):
-                self.outputs[n] = self.model(*args)
-            pool = g.pool()
-            self.graphs[n] = g
-        torch.cuda.synchronize()
-
-    def bucket(self, n: int) -> int | None:
-        return next((s for s in self.sizes if s >= n), None)
+    def capture(self, cap: _GraphCapture) -> None:
+        for n in sorted(self.sizes, reverse=True):
+            for i in range(self.model.num_layers + 1):
+                self.graphs[(i, n)], _ = cap(lambda i=i, n=n: self._stage(i, n))
 
     @torch.inference_mode()
-    def run(self, input_ids: list[int], positions: list[int], slots: list[int], block_tables: list[list[int]],
-            seq_lens: list[int]) -> torch.Tensor:  # fmt: skip
-        """Replay for a uniform decode batch; hidden states [n, hidden]."""
-        n = len(input_ids)
-        size = self.bucket(n)
-        if size is None:
-            raise ValueError(f"decode batch {n} exceeds the largest captured graph ({self.max_batch})")
-        pad = size - n
-        self.input_ids[:size].copy_(torch.tensor(input_ids + [0] * pad), non_blocking=True)
-        self.positions[:size].copy_(torch.tensor(positions + [0] * pad), non_blocking=True)
-        self.slot_mapping[:size].copy_(torch.tensor(slots + [self.scratch_slot] * pad), non_blocking=True)
-        self.seq_lens[:size].copy_(torch.tensor(seq_lens + [1] * pad), non_blocking=True)
-        width = max(len(t) for t in block_tables)
-        rows = [t + [self.scratch_block] * (width - len(t)) for t in block_tables]
-        rows += [[self.scratch_block] * width] * pad
-        self.block_tables[:size, :width].copy_(torch.tensor(rows), non_blocking=True)
-        self.graphs[size].replay()
-        return self.outputs[size][:n]
+    def run(self, n: int, positions: torch.Tensor, kv_caches: torch.Tensor, meta: AttentionMetadata) -> torch.Tensor:
+        """Final hidden states [n, hidden] of a step whose token ids are in `self.ids[:n]`."""
+        size = _bucket(self.sizes, n)
+        L = self.model.num_layers
+        for i in range(L + 1):
+            self.graphs[(i, size)].replay()
+            if i < L:
+                s = StageOut(self.resid[:n], self.qkv[:n], None)
+                self.model.attention(i, s, positions, kv_caches[i], meta, out=self.attn[:n], q_out=self.q[:n])
+        return self.resid[:n]
 
-    @torch.inference_mode()
-    def run_device(self, dm: DeviceMetadata, seqs: list[tuple[object, list[int]]], starts: list[int],
-                   input_ids: list[int]) -> torch.Tensor:  # fmt: skip
-        """`run` with the static buffers refreshed on the device from resident block tables
-        (same contents: scratch padding, the first `width` table columns)."""
-        n = len(input_ids)
-        size = self.bucket(n)
-        if size is None:
-            raise ValueError(f"decode batch {n} exceeds the largest captured graph ({self.max_batch})")
-        width = max(len(t) for _, t in seqs)
-        dm.build(seqs, starts, [1] * n, input_ids, buffers=self.buf, pad_seqs=size - n, pad_slot=self.scratch_slot,
-                 table_pad=self.scratch_block, width=width)  # fmt: skip
-        self.graphs[size].replay()
-        return self.outputs[size][:n]
+
+# -- steps ---------------------------------------------------------------------------------------
 
 
 class ModelRunner:
-    """Owns the model and the paged KV pool; runs prefill and decode steps with greedy
-    sampling. `use_graphs` replays decode steps from HIP graphs (the backend must be
-    graph-capturable)."""
+    """Owns the model's KV pool and runs steps of (sequence, tokens) with greedy sampling.
 
-    def __init__(self, model, num_blocks: int, block_size: int = 16, max_model_len: int = 4096,
-                 use_graphs: bool = True, max_graph_batch: int = 128, prefill_token_budget: int = 2048,
-                 device_metadata: bool | None = None, max_seqs: int = 1024,
+    Pool size: `num_blocks`, or as many blocks as `kv_cache_gib` GiB hold. The graph modes
+    default to on for a graph-capturable backend on the GPU (the capability the reference
+    checks as `backend is TritonAttention`, model_runner.py:47) and off otherwise;
+    `device_metadata` (default on the GPU when the backend reads the packed layout) builds step
+    inputs with kvh_prepare_metadata from resident block tables."""
+
+    def __init__(self, model: PagedLlama, *, num_blocks: int | None = None, kv_cache_gib: float | None = None,
+                 block_size: int = 16, max_model_len: int = 4096, decode_graphs: bool | None = None,
+                 piecewise_graphs: bool | None = None, max_graph_batch: int = 128, max_piecewise_tokens: int = 512,
+                 token_budget: int = 2048, device_metadata: bool | None = None, max_seqs: int = 1024,
                  kv_cache_dtype: torch.dtype | None = None):  # fmt: skip
-        cfg = model.cfg
-        p = next(model.parameters())
         self.model = model
-        self.device, self.dtype = p.device, p.dtype
-        self.block_size = block_size
-        self.max_model_len = max_model_len
-        self.num_blocks = num_blocks
-        self.scratch_block = num_blocks
-        # kv_cache_dtype: the model's dtype, or torch.float8_e4m3fn (E4M3 with each layer's
-        # k_scale / v_scale; HIP backend only)
-        self.kv_dtype = self.dtype if kv_cache_dtype is None else kv_cache_dtype
-        shape = (cfg.num_layers, 2, num_blocks + 1, block_size, cfg.num_kv_heads, cfg.head_dim)
-        if self.kv_dtype == torch.float8_e4m3fn:  # zero bytes, viewed as E4M3 (+0)
-            self.kv_caches = torch.zeros(shape, dtype=torch.uint8, device=self.device).view(self.kv_dtype)
-        else:
-            self.kv_caches = torch.zeros(shape, dtype=self.kv_dtype, device=self.device)
-        self.free_blocks = list(range(num_blocks - 1, -1, -1))
-        self.prefill_token_budget = prefill_token_budget
-        backend = model.layers[0].self_attn.backend
+        self.device = model.device
+        self.block_size, self.max_model_len = block_size, max_model_len
+        self.token_budget = token_budget
+        kv_dtype = model.dtype if kv_cache_dtype is None else kv_cache_dtype
+        if num_blocks is None:
+            if kv_cache_gib is None:
+                raise ValueError("give num_blocks or kv_cache_gib")
+            num_blocks = KVPool.blocks_in(model, kv_cache_gib, block_size, kv_dtype)
+        self.pool = KVPool(model, num_blocks, block_size, kv_dtype)
+        self.width = -(-max_model_len // block_size)
+        backend = model.backend
+        capturable = self.device.type == "cuda" and getattr(backend, "graph_capturable", False)
+        decode_graphs = capturable if decode_graphs is None else decode_graphs
+        piecewise_graphs = capturable if piecewise_graphs is None else piecewise_graphs
         self.padded_layout = getattr(backend, "needs_padded_layout", True)
-        # step inputs from block tables kept on the device (kvh_prepare_metadata) unless the
-        # backend needs the torch reference's padded layout, which only the host builds
         if device_metadata is None:
-            device_metadata = not self.padded_layout and self.device.type == "cuda"
+            device_metadata = self.device.type == "cuda" and not self.padded_layout
         if device_metadata and self.padded_layout:
-            raise ValueError("device metadata does not build the padded layout")
+            raise ValueError("device metadata does not build the torch backend's padded layout")
         self.dm = None
         if device_metadata:
-            self.dm = DeviceMetadata(self.device, max_seqs, -(-max_model_len // block_size), block_size,
-                                     max(prefill_token_budget, max_graph_batch))  # fmt: skip
-        self.graphs: DecodeGraphRunner | None = None
-        if use_graphs:
+            tokens = max(token_budget, max_graph_batch, max_piecewise_tokens if piecewise_graphs else 1)
+            self.dm = DeviceMetadata(self.device, max_seqs, self.width, block_size, tokens)
+        self.paths: Counter[str] = Counter()
+        self.decode_runner: DecodeGraphRunner | None = None
+        self.piecewise: PiecewiseGraphRunner | None = None
+        if decode_graphs or piecewise_graphs:
             if not getattr(backend, "graph_capturable", False):
                 raise ValueError(f"backend {getattr(backend, 'name', backend)} cannot be captured in a graph")
-            self.graphs = DecodeGraphRunner(model, self.kv_caches, self.scratch_block, block_size, max_graph_batch,
-                                            -(-max_model_len // block_size))  # fmt: skip
-            self.graphs.capture()
-        self.steps = {"decode_graph": 0, "eager": 0}
+            cap = _GraphCapture()
+            if piecewise_graphs:
+                ids = self.dm.buffers.input_ids if self.dm is not None else None
+                self.piecewise = PiecewiseGraphRunner(model, min(max_piecewise_tokens, token_budget), ids)
+                self.piecewise.capture(cap)
+            if decode_graphs:
+                self.decode_runner = DecodeGraphRunner(model, self.pool, max_graph_batch, self.width)
+                self.decode_runner.capture(cap)
 
-    # -- pool ----------------------------------------------------------------------------------
-    def _reserve(self, seq: Sequence, length: int) -> None:
-        need = -(-length // self.block_size) - len(seq.block_table)
-        if need > len(self.free_blocks):
-            raise RuntimeError("KV pool exhausted")
-        for _ in range(max(0, need)):
-            seq.block_table.append(self.free_blocks.pop())
+    @property
+    def kv_caches(self) -> torch.Tensor:
+        return self.pool.tensor
 
     def release(self, seq: Sequence) -> None:
-        self.free_blocks.extend(reversed(seq.block_table))
-        seq.block_table = []
+        self.pool.give_back(seq.table)
+        seq.table = []
         if self.dm is not None:
             self.dm.release(id(seq))
 
-    def slots(self, seq: Sequence, start: int, n: int) -> list[int]:
-        """Slots of positions start .. start + n - 1 (kv_cache.py:155-169)."""
-        bs, t = self.block_size, seq.block_table
-        return [t[pos // bs] * bs + pos % bs for pos in range(start, start + n)]
+    def _route(self, query_lens: list[int], num_tokens: int, eager: bool) -> str:
+        if not eager:
+            d = self.decode_runner
+            if d is not None and max(query_lens) == 1 and len(query_lens) <= d.max_batch:
+                return "decode_graph"
+            if self.piecewise is not None and num_tokens <= self.piecewise.max_tokens:
+                return "piecewise"
+        return "eager"
 
-    # -- steps -----------------------------------------------------------------------------------
     @torch.inference_mode()
-    def step(self, scheduled: list[tuple[Sequence, int]], force_eager: bool = False) -> dict[int, int]:
-        """One forward over `scheduled` (sequence, tokens to compute). Sequences whose context is
-        complete after the step get a greedy token, appended to them; returns {index: token}."""
-        ids, starts, query_lens, tables, rows, done = [], [], [], [], [], []
-        for k, (seq, n) in enumerate(scheduled):
-            start = seq.num_computed
+    def execute(self, scheduled: list[tuple[Sequence, int]], eager: bool = False) -> dict[Sequence, int]:
+        """One forward over `scheduled`; every sequence whose whole context is computed after it
+        gets its greedy next token appended. Returns {sequence: token} for those."""
+        bs = self.block_size
+        ids: list[int] = []
+        starts, qlens, last_rows, sampled = [], [], [], []
+        for seq, n in scheduled:
+            start = seq.computed
+            if n < 1 or start + n > len(seq.tokens):
+                raise ValueError(f"cannot compute {n} tokens of a sequence with {seq.pending} pending")
             if start + n > self.max_model_len:
-                raise ValueError("sequence exceeds max_model_len")
-            self._reserve(seq, start + n)
-            ids += seq.token_ids[start : start + n]
+                raise ValueError(f"sequence of {start + n} tokens exceeds max_model_len={self.max_model_len}")
+            need = -(-(start + n) // bs) - len(seq.table)
+            if need > 0:
+                seq.table += self.pool.take(need)
+            ids += seq.tokens[start : start + n]
             starts.append(start)
-            query_lens.append(n)
-            tables.append(seq.block_table)
-            if start + n == seq.num_tokens:
-                rows.append(len(ids) - 1)
-                done.append(k)
-        decode = max(query_lens) == 1
-        use_graph = self.graphs is not None and decode and not force_eager and len(ids) <= self.graphs.max_batch
+            qlens.append(n)
+            if start + n == len(seq.tokens):
+                last_rows.append(len(ids) - 1)
+                sampled.append(seq)
+        T = len(ids)
+        path = self._route(qlens, T, eager)
         if self.dm is not None:
-            keyed = [(id(seq), seq.block_table) for seq, _ in scheduled]
-            if use_graph:
-                hidden = self.graphs.run_device(self.dm, keyed, starts, ids)
+            keyed = [(id(seq), seq.table) for seq, _ in scheduled]
+            if path == "decode_graph":
+                hidden = self.decode_runner.replay_device(self.dm, keyed, starts, ids)
             else:
-                meta, ids_t, pos_t = self.dm.build(keyed, starts, query_lens, ids)
-                hidden = self.model(ids_t, pos_t, self.kv_caches, meta)
+                meta, ids_t, pos_t = self.dm.build(keyed, starts, qlens, ids)
+                if path == "piecewise":  # the stages read the shared id buffer dm.build filled
+                    hidden = self.piecewise.run(T, pos_t, self.pool.tensor, meta)
+                else:
+                    hidden = self.model(ids_t, pos_t, self.pool.tensor, meta)
         else:
-            # the reference's host path (model_runner.py:114-125, 165-197; cuda_graph.py:111-134)
+            # the reference's host path (model_runner.py:114-125, 165-197)
             pos, slots, seq_lens = [], [], []
             for (seq, n), start in zip(scheduled, starts):
                 pos += range(start, start + n)
-                slots += self.slots(seq, start, n)
+                slots += [seq.table[p // bs] * bs + p % bs for p in range(start, start + n)]
                 seq_lens.append(start + n)
-            if use_graph:
-                hidden = self.graphs.run(ids, pos, slots, tables, seq_lens)
+            tables = [seq.table for seq, _ in scheduled]
+            if path == "decode_graph":
+                hidden = self.decode_runner.replay_host(ids, pos, slots, tables, seq_lens)
             else:
-                meta = build_metadata(self.device, tables, slots, seq_lens, query_lens,
-                                      padded_layout=self.padded_layout)  # fmt: skip
-                hidden = self.model(torch.tensor(ids, device=self.device), torch.tensor(pos, device=self.device),
-                                    self.kv_caches, meta)  # fmt: skip
-        self.steps["decode_graph" if use_graph else "eager"] += 1
+                meta = build_metadata(self.device, tables, slots, seq_lens, qlens, padded_layout=self.padded_layout)
+                pos_t = torch.tensor(pos, dtype=torch.long, device=self.device)
+                if path == "piecewise":
+                    self.piecewise.ids[:T].copy_(torch.tensor(ids, dtype=torch.long), non_blocking=True)
+                    hidden = self.piecewise.run(T, pos_t, self.pool.tensor, meta)
+                else:
+                    ids_t = torch.tensor(ids, dtype=torch.long, device=self.device)
+                    hidden = self.model(ids_t, pos_t, self.pool.tensor, meta)
+        self.paths[path] += 1
         for seq, n in scheduled:
-            seq.num_computed += n
-        if not rows:
+            seq.computed += n
+        if not sampled:
             return {}
-        logits = self.model.compute_logits(hidden[torch.tensor(rows, device=self.device)])
-        tokens = logits.argmax(dim=-1).tolist()
-        out = {}
-        for k, tok in zip(done, tokens):
-            scheduled[k][0].token_ids.append(tok)
-            out[k] = tok
-        return out
+        rows = torch.tensor(last_rows, dtype=torch.long, device=self.device)
+        tokens = self.model.logits(hidden.index_select(0, rows)).argmax(dim=-1).tolist()
+        for seq, tok in zip(sampled, tokens):
+            seq.tokens.append(tok)
+        return dict(zip(sampled, tokens))
 
+    # convenience for benchmarks: whole batches in lockstep
     def prefill(self, seqs: list[Sequence]) -> None:
-        """Compute every prompt in chunks of at most the token budget per step (chunked
-        prefill); the last chunk of each prompt yields its first generated token."""
-        while True:
-            budget, sched = self.prefill_token_budget, []
-            for seq in seqs:
-                n = min(seq.prompt_len - seq.num_computed, budget)
+        """Compute the rest of every sequence's prompt, chunked to the token budget per step; the
+        step that completes a prompt samples its first token."""
+        while any(s.computed < s.prompt_len for s in seqs):
+            room, step = self.token_budget, []
+            for s in seqs:
+                n = min(s.prompt_len - s.computed, room)
                 if n > 0:
-                    sched.append((seq, n))
-                    budget -= n
-                if budget == 0:
+                    step.append((s, n))
+                    room -= n
+                if room == 0:
                     break
-            if not sched:
-                return
-            self.step(sched)
+            self.execute(step)
 
-    def decode(self, seqs: list[Sequence], force_eager: bool = False) -> list[int]:
-        """One token for every sequence (each has exactly one uncomputed token)."""
-        res = self.step([(s, 1) for s in seqs], force_eager=force_eager)
-        return [res[k] for k in range(len(seqs))]
+    def decode(self, seqs: list[Sequence], eager: bool = False) -> list[int]:
+        """One token for each sequence (each has exactly one token pending)."""
+        got = self.execute([(s, 1) for s in seqs], eager=eager)
+        return [got[s] for s in seqs]
 
-    def generate(self, prompts: list[list[int]], max_new_tokens: int, force_eager: bool = False) -> list[list[int]]:
-        """Greedy generation; returns the generated tokens of each prompt."""
-        seqs = [Sequence(list(p)) for p in prompts]
-        self.prefill(seqs)
-        for _ in range(max_new_tokens - 1):
-            self.decode(seqs, force_eager=force_eager)
-        out = [s.token_ids[len(p):] for s, p in zip(seqs, prompts)]
-        for s in seqs:
-            self.release(s)
-        return out
+
+class Batcher:
+    """Scheduler-free continuous batching: every step spends at most `token_budget` tokens,
+    first on the sequences already admitted (a decode token, or the next chunk of a prompt
+    still being computed), oldest first, then on newly submitted prompts in arrival order,
+    chunked to what the budget leaves. Finished sequences release their blocks."""
+
+    def __init__(self, runner: ModelRunner, token_budget: int | None = None, max_seqs: int = 256):
+        self.runner = runner
+        self.budget = token_budget or runner.token_budget
+        self.max_seqs = max_seqs
+        self.admitted: list[Sequence] = []
+        self.queue: list[Sequence] = []
+
+    def submit(self, prompt: list[int], max_new_tokens: int) -> Sequence:
+        seq = Sequence(list(prompt), max_new_tokens)
+        self.queue.append(seq)
+        return seq
+
+    @property
+    def busy(self) -> bool:
+        return bool(self.admitted or self.queue)
+
+    def step(self, eager: bool = False) -> list[Sequence]:
+        """Run one step; returns the sequences it finished."""
+        room, plan = self.budget, []
+        for seq in self.admitted:
+            if room == 0:
+                break
+            n = min(seq.pending, room)
+            plan.append((seq, n))
+            room -= n
+        while self.queue and room > 0 and len(self.admitted) < self.max_seqs:
+            seq = self.queue.pop(0)
+            self.admitted.append(seq)
+            n = min(seq.pending, room)
+            plan.append((seq, n))
+            room -= n
+        if not plan:
+            return []
+        self.runner.execute(plan, eager=eager)
+        done = [s for s in self.admitted if s.finished]
+        for s in done:
+            self.admitted.remove(s)
+            self.runner.release(s)
+        return done
+
+    def drain(self, eager: bool = False) -> None:
+        while self.busy:
+            self.step(eager)
+
+
+def generate(runner: ModelRunner, prompts: list[list[int]], max_new_tokens: int, eager: bool = False,
+             token_budget: int | None = None) -> list[list[int]]:  # fmt: skip
+    """Greedy generation of all prompts together through a Batcher; the generated tokens."""
+    b = Batcher(runner, token_budget)
+    seqs = [b.submit(p, max_new_tokens) for p in prompts]
+    b.drain(eager)
+    return [s.generated for s in seqs]

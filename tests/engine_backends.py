@@ -4,9 +4,18 @@ static-method interface as HipAttention. Test infrastructure only."""
 
 from __future__ import annotations
 
+from types import SimpleNamespace
+
 import torch
 
+from kvserve_amd.engine.model import rope_tables
 from oracle import fp8, torch_reference
+
+
+def rope(cfg, max_positions: int, device=None) -> SimpleNamespace:
+    """The model's fp32 cos / sin tables as `.cos` / `.sin` [max_positions, head_dim]."""
+    cos, sin = rope_tables(cfg, max_positions, device)
+    return SimpleNamespace(cos=cos, sin=sin)
 
 
 class TorchRefAttention:

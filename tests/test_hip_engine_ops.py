@@ -13,8 +13,10 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from kvserve_amd import HipAttention
 from kvserve_amd.engine import LLAMA_3_2_1B, ops
-from kvserve_amd.engine.model import build_model
+from kvserve_amd.engine.model import PagedLlama, random_weights
+from kvserve_amd.engine.runner import ModelRunner, Sequence
 
 pytestmark = pytest.mark.gpu
 
@@ -142,22 +144,29 @@ def test_gemv_strided_rows_and_large_batches_fall_back(hip_device):
 
 
 def test_fused_model_matches_the_unfused_model(hip_device):
-    """The same bf16 weights through piece() with and without the fused kernels: logits of a
-    prefill and of decode-sized batches (the GEMV path) agree within bf16 accuracy."""
+    """The same bf16 weights with and without libkvhip's layer kernels, through whole steps over a
+    KV pool (cache write + paged attention in every layer): a prefill of T prompts, then a decode
+    step of T rows -- T = 1 and 4 (GEMV; projection + RoPE + cache write in one kernel), 5, 48 and
+    64 (skinny MFMA projections; the fused QKV + RoPE + cache write) and 80 (hipBLASLt). Logits
+    of both steps agree within bf16 accuracy."""
     cfg = LLAMA_3_2_1B.with_layers(2)
-    models = [build_model(cfg, hip_device, torch.bfloat16, 512, seed=7, std=0.03, fused_ops=f) for f in (True, False)]
+    w = random_weights(cfg, hip_device, torch.bfloat16, seed=7, std=0.03)
+    models = [PagedLlama(cfg, w, HipAttention, 512, fused_ops=f) for f in (True, False)]
     assert models[0].fused_ops and not models[1].fused_ops
-    for T in (1, 5, 64):
-        ids = torch.arange(T, device=hip_device) * 131 % cfg.vocab_size
-        outs = []
+    assert models[0].defers_projection(48) and not models[1].defers_projection(48)
+    for T in (1, 4, 5, 48, 64, 80):
+        logits = []
         for mdl in models:
-            with torch.inference_mode():
-                x, qkv, h0, _ = mdl.piece(0, ids, None, None, None)
-                if qkv is None:  # decode-sized: the projection runs in the attention step
-                    qkv = ops.linear(h0, mdl.layers[0].self_attn.qkv_proj.weight)
-                attn = qkv[:, : cfg.num_heads * cfg.head_dim].reshape(T, cfg.num_heads, cfg.head_dim)
-                h, _, _, _ = mdl.piece(1, ids, None, x, attn)
-                x2, _, _, _ = mdl.piece(2, ids, None, h, attn)
-                outs.append(mdl.compute_logits(x2))
-        scale = outs[1].abs().max().item()
-        assert (outs[0] - outs[1]).abs().max().item() <= 0.03 * scale, T
+            r = ModelRunner(mdl, num_blocks=T * 2 + 4, max_model_len=512, decode_graphs=False, piecewise_graphs=False)
+            seqs = [Sequence([(131 * i + 7 * j) % cfg.vocab_size for j in range(11)]) for i in range(T)]
+            got = []
+            orig = mdl.logits
+            mdl.logits = lambda h, _o=orig, _g=got: _g.append(_o(h)) or _g[-1]
+            try:
+                r.prefill(seqs)
+                r.decode(seqs)
+            finally:
+                mdl.logits = orig
+            logits.append(torch.cat(got))
+        scale = logits[1].abs().max().item()
+        assert (logits[0] - logits[1]).abs().max().item() <= 0.03 * scale, T

@@ -19,7 +19,7 @@ import torch
 from kvserve_amd import HipAttention, last_launch_kernels, workloads
 from kvserve_amd.attention import AttentionMetadata
 from kvserve_amd.engine import LLAMA_3_2_1B
-from kvserve_amd.engine.model import RotaryEmbedding
+from tests.engine_backends import rope as rope_table
 from oracle import fp8, torch_reference
 from tests import paged_check as pc
 
@@ -97,7 +97,7 @@ def test_rope_and_cache_fp8_bit_exact(hip_device, dtype):
     k_scale, v_scale = 0.75, 1.5
     gen = torch.Generator(device=hip_device).manual_seed(11)
     qkv = (torch.randn(T, (H + 2 * Hkv) * D, generator=gen, device=hip_device) * 40).to(dtype)
-    rope = RotaryEmbedding(dataclasses.replace(LLAMA_3_2_1B, head_dim=D), 4096, device=hip_device)
+    rope = rope_table(dataclasses.replace(LLAMA_3_2_1B, head_dim=D), 4096, device=hip_device)
     pos = torch.randint(0, 4096, (T,), generator=gen, device=hip_device)
     slots = torch.randperm(NB * BS, generator=gen, device=hip_device)[:T]
     kc = torch.zeros((NB, BS, Hkv, D), dtype=torch.uint8, device=hip_device).view(FP8)

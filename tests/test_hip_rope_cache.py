@@ -11,7 +11,7 @@ import torch
 
 from kvserve_amd import HipAttention
 from kvserve_amd.engine import LLAMA_3_2_1B
-from kvserve_amd.engine.model import RotaryEmbedding
+from tests.engine_backends import rope as rope_table
 from oracle import torch_reference
 
 pytestmark = pytest.mark.gpu
@@ -23,7 +23,7 @@ def _case(dtype, H, Hkv, D, T, num_blocks=64, BS=16, max_pos=4096, extra=0, seed
     width = (H + 2 * Hkv) * D
     buf = torch.randn(T, width + extra, generator=g, device=dev).to(dtype)
     qkv = buf[:, :width]  # a strided view when extra > 0
-    rope = RotaryEmbedding(dataclasses.replace(LLAMA_3_2_1B, head_dim=D), max_pos, device=dev)
+    rope = rope_table(dataclasses.replace(LLAMA_3_2_1B, head_dim=D), max_pos, device=dev)
     positions = torch.randint(0, max_pos, (T,), generator=g, device=dev)
     slots = torch.randperm(num_blocks * BS, generator=g, device=dev)[:T]
     kc = torch.randn(num_blocks, BS, Hkv, D, generator=g, device=dev).to(dtype)
@@ -103,7 +103,7 @@ def test_gemv_rope_and_cache_is_gemv_then_rope_and_cache(hip_device, dtype, m, H
     g = torch.Generator(device=hip_device).manual_seed(m * D + k + fp8)
     x = torch.randn(m, k, generator=g, device=hip_device).to(dtype)
     w = (torch.randn((H + 2 * Hkv) * D, k, generator=g, device=hip_device) * 0.05).to(dtype)
-    rope = RotaryEmbedding(dataclasses.replace(LLAMA_3_2_1B, head_dim=D), 4096, device=hip_device)
+    rope = rope_table(dataclasses.replace(LLAMA_3_2_1B, head_dim=D), 4096, device=hip_device)
     pos = torch.randint(0, 4096, (m,), generator=g, device=hip_device)
     NB, BS = 32, 16
     slots = torch.randperm(NB * BS, generator=g, device=hip_device)[:m]

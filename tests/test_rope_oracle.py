@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from kvserve_amd.engine import LLAMA_3_2_1B
-from kvserve_amd.engine.model import RotaryEmbedding
+from tests.engine_backends import rope as rope_table
 from oracle import torch_reference
 
 transformers = pytest.importorskip("transformers")
@@ -31,7 +31,7 @@ def test_rope_matches_transformers(dtype):
     want = hf.apply_rotary_pos_emb(q.transpose(0, 1)[None], q.transpose(0, 1)[None], cos_hf, sin_hf)[0][0]
     want = want.transpose(0, 1)
     # the oracle, fed with fp32 tables of the same frequencies
-    table = RotaryEmbedding(cfg, 4096)
+    table = rope_table(cfg, 4096)
     got = torch_reference.rope(q, table.cos, table.sin, positions)
     assert torch.equal(got, want)
 
@@ -41,7 +41,7 @@ def test_planted_mistake_is_caught():
     the halves' signs swapped (a plausible slip) gives different values."""
     g = torch.Generator().manual_seed(1)
     x = torch.randn(5, 2, 8, generator=g)
-    table = RotaryEmbedding(dataclasses.replace(LLAMA_3_2_1B, head_dim=8), 64)
+    table = rope_table(dataclasses.replace(LLAMA_3_2_1B, head_dim=8), 64)
     pos = torch.tensor([0, 1, 7, 30, 63])
     r = torch_reference.rope(x, table.cos, table.sin, pos)
     torch.testing.assert_close(r.norm(dim=-1), x.norm(dim=-1))
