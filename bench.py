@@ -48,6 +48,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
 BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
+FLUSH_BYTES = 1 << 30  # written before each HBM-cold timed call
 METRIC = "paged-attn decode HBM GB/s (% peak) + prefill TFLOP/s; 1B/8B decode tok/s"
 
 
@@ -123,19 +124,35 @@ def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0, f
     torch.cuda.synchronize()
     ms_step = start.elapsed_time(end) / steps
 
-    # per-kernel durations from events the library records around each launch
+    # HBM-cold timings: a 1 GiB write before each timed call evicts the 256 MB Infinity Cache
+    # and the L2s (the reference flushes 256 MB for a 72 MB L2, bench/bench_kernel.py:36)
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda:0")
+    cold = []
+    for _ in range(max(5, min(steps, 20))):
+        flush.zero_()
+        start.record()
+        step()
+        end.record()
+        end.synchronize()
+        cold.append(start.elapsed_time(end))
+    ms_step_cold = statistics.median(cold)
+
+    # per-kernel durations from events the library records around each launch, each call
+    # after a flush
     lib = _lib.load()
     ev = HipEvents(5)
     per_kernel: dict[str, list[float]] = {}
     HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping, **kw)
     for _ in range(prof_iters):
+        flush.zero_()
         lib.kvh_profile_arm(ev.array, 5)
         HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale, **kw)
         kinds = last_launch_kernels()
         for k, kind in enumerate(kinds[:4]):
             per_kernel.setdefault(kind, []).append(ev.elapsed_ms(k, k + 1))
     ev.close()
-    kernel_ms = {k: statistics.mean(v) for k, v in per_kernel.items()}
+    del flush
+    kernel_ms = {k: statistics.median(v) for k, v in per_kernel.items()}
 
     attn_bytes = w.algorithmic_bytes(elem, unique=True, kv_elem_bytes=kv_elem)
     # the cache write reads 16-bit rows and writes kv_elem-byte rows
@@ -144,6 +161,8 @@ def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0, f
         "workload": w.name + ("_fp8kv" if fp8 else ""),
         "ms_per_step": ms_step,
         "step_gbs": step_bytes / (ms_step * 1e-3) / 1e9,
+        "ms_per_step_cold": ms_step_cold,
+        "step_gbs_cold": step_bytes / (ms_step_cold * 1e-3) / 1e9,
         "attn_bytes": attn_bytes,
         "kernel_ms": kernel_ms,
         "kernels": kinds,
@@ -512,10 +531,24 @@ def main() -> int:
         sec = {}
         runs = [(idx, False) for idx in (1, 3, 4, 5)] + [(idx, True) for idx in (2, 3, 4)]
         for idx, kv8 in runs:
-            r = measure(idx, max(5, args.steps // 5), 2, max(5, args.prof_iters // 2), fp8=kv8)
+            r = measure(idx, max(20, args.steps), 3, max(10, args.prof_iters), fp8=kv8)
             print(f"# c{idx}{' fp8 kv' if kv8 else ''}: {r}", file=sys.stderr, flush=True)
             sec[r["workload"]] = {k: v for k, v in r.items() if k not in ("workload", "attn_bytes")}
         record["secondary"] = sec
+        c3 = sec.get("c3_mixed_prefill", {})
+        if "prefill_tflops" in c3:
+            record["roofline_prefill"] = {
+                "bound": "mfma",
+                "achieved": c3["prefill_tflops"],
+                "peak": BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": c3["prefill_tflops"] / BF16_PEAK_TFLOPS,
+                "traffic": None,
+                "kernel": "pa_prefill_kernel<BF16,128,false> (stream-K prefill tiles)",
+                "kernel_ms": c3["kernel_ms"]["prefill"],
+                "workload": "c3_mixed_prefill: the 4 prefill chunks of 384 tokens (HBM-cold, median)",
+                "gflop": c3["prefill_gflop"],
+            }
     if not args.no_secondary:
         meta = {}
         for idx in (2, 3):

@@ -406,6 +406,7 @@ static int paged_attention_impl(const void* q, int64_t q_tok_stride, int64_t q_h
   p.NUP = 0;  // set by the prefill launcher likewise
   p.CASC = 0;  // set by the launcher when the plan has the cascade path
   p.SG = plan.SG;
+  p.PR = kPrefillRows;  // the prefill launcher sets its own tile rows
   if (plan.ws_bytes) {
     char* w = (char*)workspace;
     p.ws_acc = (float*)w;

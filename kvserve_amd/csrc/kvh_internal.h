@@ -12,7 +12,9 @@ namespace kvh {
 constexpr int32_t kMaxDecodeWaves = 8192;
 // Upper bound on the workgroups (work units) of one prefill launch: 256 CUs x 3 resident.
 constexpr int32_t kMaxPrefillUnits = 768;
-// Query rows ((token, head) pairs of one kv head) one prefill workgroup owns.
+// Query rows ((token, head) pairs of one kv head) of one prefill workgroup's tile; the
+// prefill workspace holds 2 slots x kMaxPrefillUnits x kPrefillRows partial rows, and a
+// launch's units x 2 x its tile rows (PAParams::PR) stay within that.
 constexpr int32_t kPrefillRows = 128;
 // Cascade decode over a shared prefix: planned when a decode-only batch has at most 16 query
 // rows per sequence (one 16-row tile) and block tables longer than kCascadeMinTokens; used
@@ -53,11 +55,12 @@ struct PAParams {
   int32_t PLAN;    // 1: workgroup 0 of the decode launch writes the prefill plan
   int32_t CASC;    // 1: the share kernel ran before the decode launch (cascade over a shared prefix)
   int32_t SG;      // cascade: decode-class sequences per 16-row prefix group (16 / RS)
+  int32_t PR;      // query rows ((token, head) pairs of one kv head) per prefill tile
   float v_scale;   // factor of every output row: the V scale of an E4M3 cache, else 1
   float* ws_acc;   // [slots, HGW, RS, D] unnormalised partial outputs of split decode segments
   float* ws_ml;    // [slots, HGW, RS, 2] running max (exp2 domain) and sum of each partial
-  float* ws_pacc;  // [2 kMaxPrefillUnits, kPrefillRows, D] partial outputs of split prefill tiles
-  float* ws_pml;   // [2 kMaxPrefillUnits, kPrefillRows, 2]
+  float* ws_pacc;  // [2 NUP, PR, D] partial outputs of split prefill tiles (capacity: kPrefillRows)
+  float* ws_pml;   // [2 NUP, PR, 2]
   int32_t* ws_job; // [kMaxJobs, kJobInts] merge jobs, rewritten by every unit on every call
   // prefill plan, written by pa_plan_kernel before the prefill launch:
   int64_t* ws_plan_hdr;  // [4]: flat size C, active units NUa, prefill sequences n_pre

@@ -1074,13 +1074,13 @@ __device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job,
   const int kind = job[0];
   if (kind == kJobNone) return;
   const bool dec = kind == kJobDecode;
-  const int rows = dec ? p.HGW * p.RS : kPrefillRows;
+  const int rows = dec ? p.HGW * p.RS : p.PR;
   const int pieces = job[1];
   const int64_t slot0 = job[2], slotb = job[3];
   const int stride = job[4];
   const int64_t qs = job[5];
   const int R = job[6], rbase = job[7], kvh0 = job[8];
-  const int rph = dec ? p.RS : kPrefillRows;  // rows per head
+  const int rph = dec ? p.RS : p.PR;  // rows per head
   // only the rows that reach the output: rv = min(rph, R - rbase) of each head's rph; the
   // workgroup's 16 are valid rows x0 .. x0 + 15, valid row v being piece row (v / rv) rph + v % rv
   const int rv = min(rph, R - rbase);
@@ -1214,9 +1214,9 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
   } else {
     if constexpr (!MIXED) return;
     const int bp = b - p.NU * CD;
-    if (bp >= p.NUP * (kPrefillRows / MR)) return;
-    job = p.ws_job + ((int64_t)kMaxDecodeWaves + bp / (kPrefillRows / MR)) * kJobInts;
-    chunk = bp % (kPrefillRows / MR);
+    if (bp >= p.NUP * (p.PR / MR)) return;
+    job = p.ws_job + ((int64_t)kMaxDecodeWaves + bp / (p.PR / MR)) * kJobInts;
+    chunk = bp % (p.PR / MR);
   }
   merge_job<E, D, F>(p, job, chunk, casc);
 }
@@ -1845,7 +1845,7 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
 // Chunks of tile t (rows 128 t .. of R): those its last row can see, at least one so that
 // every tile is visited and written.
 __device__ __forceinline__ int pre_tile_chunks(const PAParams& p, const SeqView& sv, int R, int t) {
-  const int last = min(kPrefillRows * t + kPrefillRows - 1, R - 1);
+  const int last = min(p.PR * t + p.PR - 1, R - 1);
   const int lim = (int)clamp64(sv.ctx + last / p.G + 1, 0, sv.kv_total);
   return max(1, (lim + kChunk - 1) / kChunk);
 }
@@ -1858,7 +1858,7 @@ constexpr int kTileCost = 4;
 __device__ __forceinline__ int64_t pre_seq_chunks(const PAParams& p, const SeqView& sv) {
   if (sv.q_len <= p.QS) return 0;
   const int R = sv.q_len * p.G;
-  const int tiles = (R + kPrefillRows - 1) / kPrefillRows;
+  const int tiles = (R + p.PR - 1) / p.PR;
   int64_t n = 0;
   for (int t = 0; t < tiles; ++t) n += kTileCost + pre_tile_chunks(p, sv, R, t);
   return n;
@@ -1960,11 +1960,10 @@ __device__ void plan_prefill(const PAParams& p) {
 // dealt to the 8 XCDs round-robin, so the units are numbered XCD by XCD: the units of one
 // XCD are contiguous in the flat space and read the same sequence's K/V through that
 // XCD's L2.
-template <class E, int D, bool KV8>
-__global__ __launch_bounds__(256, KV8 ? 2 : 3) void pa_prefill_kernel(PAParams p) {
-  using L = PrefillLds<D>;
-  __shared__ __attribute__((aligned(1024))) char lds[(KV8 ? 2 : L::kStages) * L::kStageBytes];
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+// The units' walk over the flat space (shared by both prefill kernels): `tile(sv, R, seq,
+// kvh, t, c_lo, c_hi, partial, slot, rest, total)` computes chunks [c_lo, c_hi) of tile t.
+template <class TileFn>
+__device__ __forceinline__ void prefill_units(const PAParams& p, TileFn&& tile) {
   int32_t* job = p.ws_job + (int64_t)(kMaxDecodeWaves + blockIdx.x) * kJobInts;
   if (threadIdx.x == 0) job[0] = kJobNone;
 
@@ -1986,7 +1985,7 @@ __global__ __launch_bounds__(256, KV8 ? 2 : 3) void pa_prefill_kernel(PAParams p
   int seq = uni(p.ws_pre_list[k]);
   SeqView sv = seq_view_uniform(p, seq);
   int R = sv.q_len * p.G;
-  int tiles = (R + kPrefillRows - 1) / kPrefillRows;
+  int tiles = (R + p.PR - 1) / p.PR;
   int n_t = pre_tile_chunks(p, sv, R, t);
   int64_t rem = uni(ud[3]);
   // a: this unit's first position within the tile. Positions a .. b - 1 of a tile are its
@@ -2003,15 +2002,12 @@ __global__ __launch_bounds__(256, KV8 ? 2 : 3) void pa_prefill_kernel(PAParams p
       const bool whole = c_lo == 0 && c_hi == n_t;
       const int64_t slot = 2 * (int64_t)u + (first ? 0 : 1);
       const int rest = (int)(x1 - (x + (b - a))), total = (int)(x1 - (u * C / NUa));
-      if constexpr (KV8)
-        prefill_tile_kv8<E, D>(lds, p, sv, R, seq, kvh, t, c_lo, c_hi, w, !whole, slot, rest, total);
-      else
-        prefill_tile<E, D>(lds, p, sv, R, seq, kvh, t, c_lo, c_hi, w, !whole, slot, rest, total);
+      tile(sv, R, seq, kvh, t, c_lo, c_hi, !whole, slot, rest, total);
       if (threadIdx.x == 0 && c_lo == 0 && c_hi < n_t) {
         // the tile continues in units u + 1 .. u1, each holding it as its first piece
         const int64_t x_last = x + (tw - a) - 1;
         const int64_t u1 = ((x_last + 1) * NUa - 1) / C;
-        write_job(job, kJobPrefill, (int)(u1 - u + 1), slot, 2 * (int64_t)u, 2, sv.qs, R, t * kPrefillRows, kvh);
+        write_job(job, kJobPrefill, (int)(u1 - u + 1), slot, 2 * (int64_t)u, 2, sv.qs, R, t * p.PR, kvh);
       }
       first = false;
     }
@@ -2026,17 +2022,32 @@ __global__ __launch_bounds__(256, KV8 ? 2 : 3) void pa_prefill_kernel(PAParams p
         seq = uni(p.ws_pre_list[k]);
         sv = seq_view_uniform(p, seq);
         R = sv.q_len * p.G;
-        tiles = (R + kPrefillRows - 1) / kPrefillRows;
+        tiles = (R + p.PR - 1) / p.PR;
       }
     }
     n_t = pre_tile_chunks(p, sv, R, t);
   }
 }
 
+// 4-wave workgroups of kPrefillRows = 128 rows (PAParams::PR).
+template <class E, int D, bool KV8>
+__global__ __launch_bounds__(256, KV8 ? 2 : 3) void pa_prefill_kernel(PAParams p) {
+  using L = PrefillLds<D>;
+  __shared__ __attribute__((aligned(1024))) char lds[(KV8 ? 2 : L::kStages) * L::kStageBytes];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  prefill_units(p, [&](const SeqView& sv, int R, int seq, int kvh, int t, int c_lo, int c_hi, bool partial,
+                       int64_t slot, int rest, int total) {
+    if constexpr (KV8)
+      prefill_tile_kv8<E, D>(lds, p, sv, R, seq, kvh, t, c_lo, c_hi, w, partial, slot, rest, total);
+    else
+      prefill_tile<E, D>(lds, p, sv, R, seq, kvh, t, c_lo, c_hi, w, partial, slot, rest, total);
+  });
+}
+
 // ---------------------------------------------------------------------------------------
 // Workgroups of 256 threads one launch of `kernel` can keep resident on the current device
 // (cached per device and kernel).
-static int resident_blocks(const void* kernel) {
+static int resident_blocks(const void* kernel, int block_threads = 256) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
   struct Entry {
@@ -2050,7 +2061,8 @@ static int resident_blocks(const void* kernel) {
     if (cache[i].dev == dev && cache[i].kernel == kernel) return cache[i].blocks;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu <= 0) per_cu = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block_threads, 0) != hipSuccess || per_cu <= 0)
+    per_cu = 1;
   const int blocks = cus * per_cu;
   if (cache_n < 8) cache[cache_n++] = Entry{dev, kernel, blocks};
   return blocks;
@@ -2080,9 +2092,12 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipSt
     log.after_launch(5, s);
   }
   if (plan.launch_prefill) {
-    // the unit count is fixed before the decode launch: both kernels write merge jobs
+    // the unit count is fixed before the decode launch: both kernels write merge jobs. Units x
+    // 2 partial slots x tile rows stay within the workspace's kMaxPrefillUnits x 2 x kPrefillRows.
+    p.PR = kPrefillRows;
     int units = resident_blocks((const void*)&pa_prefill_kernel<E, D, KV8>);
-    if (units > kMaxPrefillUnits) units = kMaxPrefillUnits;
+    const int cap = kMaxPrefillUnits * kPrefillRows / p.PR;
+    if (units > cap) units = cap;
     p.NUP = units / 8 * 8;
     if (p.NUP < 8) p.NUP = 8;
   }
@@ -2103,7 +2118,7 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipSt
   const int mr = plan.launch_prefill ? merge_rows_decode<D, true>() : merge_rows_decode<D, false>();
   const int cd = (p.HGW * p.RS + mr - 1) / mr;
   const int nseg = plan.cascade ? p.B * (p.Hkv / p.HGW) : 0;  // cascade records
-  const dim3 mg((p.NU > nseg ? p.NU : nseg) * cd + p.NUP * (kPrefillRows / merge_rows<D, 2>()));
+  const dim3 mg((p.NU > nseg ? p.NU : nseg) * cd + p.NUP * (p.PR / merge_rows<D, 2>()));
   if (plan.launch_prefill)
     hipLaunchKernelGGL((pa_merge_kernel<E, D, true>), mg, dim3(256), 0, s, p);
   else
