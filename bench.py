@@ -124,12 +124,15 @@ def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0, f
     torch.cuda.synchronize()
     ms_step = start.elapsed_time(end) / steps
 
-    # HBM-cold timings: a 1 GiB write before each timed call evicts the 256 MB Infinity Cache
-    # and the L2s (the reference flushes 256 MB for a 72 MB L2, bench/bench_kernel.py:36)
-    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda:0")
+    # HBM-cold timings: a 1 GiB read before each timed call evicts the 256 MB Infinity Cache
+    # and the L2s (the reference flushes 256 MB for a 72 MB L2, bench/bench_kernel.py:36). A
+    # read, not a write: written lines would stay dirty in the caches and their write-back
+    # would be charged to the timed kernel.
+    flush = torch.zeros(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda:0")
+    torch.cuda.synchronize()
     cold = []
     for _ in range(max(5, min(steps, 20))):
-        flush.zero_()
+        flush.amax()
         start.record()
         step()
         end.record()
@@ -144,7 +147,7 @@ def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0, f
     per_kernel: dict[str, list[float]] = {}
     HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping, **kw)
     for _ in range(prof_iters):
-        flush.zero_()
+        flush.amax()
         lib.kvh_profile_arm(ev.array, 5)
         HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale, **kw)
         kinds = last_launch_kernels()
