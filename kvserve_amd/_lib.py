@@ -129,6 +129,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
 }
 
 _lib: ctypes.CDLL | None = None
+_fast = None
 _lock = threading.Lock()
 
 
@@ -160,8 +161,24 @@ def load() -> ctypes.CDLL:
         version = lib.kvh_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"libkvhip ABI {version} does not match the Python binding ({ABI_VERSION})")
+        global _fast
+        try:
+            from kvserve_amd import _kvhfast
+        except ImportError as e:
+            raise RuntimeError(
+                f"kvserve_amd/_kvhfast is not built ({e}): build it with `python -m kvserve_amd.build`."
+            ) from e
+        _kvhfast.bind(lib._handle)
+        _fast = _kvhfast
         _lib = lib
     return _lib
+
+
+def fast():
+    """The METH_FASTCALL binding of the per-step entry points, bound to the loaded library."""
+    if _fast is None:
+        load()
+    return _fast
 
 
 def strerror(status: int) -> str:

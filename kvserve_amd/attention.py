@@ -71,7 +71,7 @@ def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
 
 # Per-call host work matters at decode sizes (tens of microseconds against kernels of the same
 # order), so what depends only on the cache tensors' layout is checked once per layout and
-# kept: (num_blocks, block_size, kv_heads, head_dim, k strides, v strides as ctypes arrays).
+# kept: (num_blocks, block_size, kv_heads, head_dim, k strides, v strides, device index).
 _CACHE_LAYOUTS: dict = {}
 _WS_SIZES: dict = {}
 
@@ -87,7 +87,7 @@ def _cache_layout(k_cache: torch.Tensor, v_cache: torch.Tensor) -> tuple:
         _require(k_cache.get_device() == v_cache.get_device(), "k_cache and v_cache are on different devices")
         if len(_CACHE_LAYOUTS) > 256:
             _CACHE_LAYOUTS.clear()
-        hit = (*k_cache.shape, _lib.i64x3(ks[:3]), _lib.i64x3(vs[:3]), k_cache.get_device())
+        hit = (*k_cache.shape, tuple(ks[:3]), tuple(vs[:3]), k_cache.get_device())
         _CACHE_LAYOUTS[key] = hit
     return hit
 
@@ -169,21 +169,21 @@ class HipAttention:
         _require(k.stride(-1) == 1 and v.stride(-1) == 1, "k/v last dim must be contiguous")
         _check_index(slots, "slot_mapping", 1)
         _require(slots.shape[0] == k.shape[0], "one slot per token")
-        lib = _lib.load()
+        fast = _lib.fast()
         if fp8:
             dtype = _dtype_code(k, v)
-            st = lib.kvh_reshape_and_cache_fp8(
+            st = fast.reshape_and_cache_fp8(
                 k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
-                k_cache.data_ptr(), kcs, v_cache.data_ptr(), vcs, slots.data_ptr(), k.shape[0], num_blocks,
+                k_cache.data_ptr(), *kcs, v_cache.data_ptr(), *vcs, slots.data_ptr(), k.shape[0], num_blocks,
                 num_kv_heads, head_dim, block_size, dtype, float(k_scale), float(v_scale),
                 _stream_handle(k_cache.device),
             )  # fmt: skip
             _lib.check(st, "kvh_reshape_and_cache_fp8")
             return
         dtype = _dtype_code(k_cache, v_cache, k, v)
-        st = lib.kvh_reshape_and_cache(
+        st = fast.reshape_and_cache(
             k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
-            k_cache.data_ptr(), kcs, v_cache.data_ptr(), vcs,
+            k_cache.data_ptr(), *kcs, v_cache.data_ptr(), *vcs,
             slots.data_ptr(), k.shape[0], num_blocks, num_kv_heads, head_dim, block_size, dtype,
             _stream_handle(k_cache.device),
         )  # fmt: skip
@@ -234,19 +234,14 @@ class HipAttention:
         dtype = _dtype_code(qkv, out) if fp8 else _dtype_code(qkv, k_cache, v_cache, out)
         if num_tokens == 0:
             return out
-        args = [
+        st = _lib.fast().rope_and_cache(
             qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
             out.data_ptr(), out.stride(0), out.stride(1),
-            k_cache.data_ptr(), kcs, v_cache.data_ptr(), vcs,
+            k_cache.data_ptr(), *kcs, v_cache.data_ptr(), *vcs,
             slots.data_ptr(), num_tokens, num_blocks, num_heads, num_kv_heads, head_dim, block_size, dtype,
-        ]  # fmt: skip
-        lib = _lib.load()
-        if fp8:
-            st = lib.kvh_rope_and_cache_fp8(*args, float(k_scale), float(v_scale), _stream_handle(qkv.device))
-            _lib.check(st, "kvh_rope_and_cache_fp8")
-        else:
-            st = lib.kvh_rope_and_cache(*args, _stream_handle(qkv.device))
-            _lib.check(st, "kvh_rope_and_cache")
+            int(fp8), float(k_scale), float(v_scale), _stream_handle(qkv.device),
+        )  # fmt: skip
+        _lib.check(st, "kvh_rope_and_cache_fp8" if fp8 else "kvh_rope_and_cache")
         return out
 
     # rows up to which gemv_rope_and_cache applies (up to 4 on the GEMV, then on the MFMA units)
@@ -294,7 +289,7 @@ class HipAttention:
             x.data_ptr(), x.stride(0), w_qkv.data_ptr(), w_qkv.stride(0), num_tokens, hidden,
             positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
             out.data_ptr(), out.stride(0), out.stride(1),
-            k_cache.data_ptr(), kcs, v_cache.data_ptr(), vcs,
+            k_cache.data_ptr(), _lib.i64x3(kcs), v_cache.data_ptr(), _lib.i64x3(vcs),
             slots.data_ptr(), num_blocks, num_heads, num_kv_heads, head_dim, block_size, dtype, int(fp8),
             float(k_scale), float(v_scale), _stream_handle(x.device),
         )  # fmt: skip
@@ -341,21 +336,24 @@ class HipAttention:
         ws_bytes = _workspace_size(lib, num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, width, block_size, max_q,
                                    dtype)  # fmt: skip
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
-        head = [
-            q.data_ptr(), q.stride(0), q.stride(1),
-            k_cache.data_ptr(), kcs, v_cache.data_ptr(), vcs,
-            num_blocks,
-            out.data_ptr(), out.stride(0), out.stride(1),
-            tables.data_ptr(), tables.stride(0), width,
-            seq_lens.data_ptr(), qsl.data_ptr(),
-            num_tokens, num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_q, float(scale),
-        ]  # fmt: skip
-        tail = [ws.data_ptr() if ws is not None else None, ws_bytes, _stream_handle(q.device)]
+        fast = _lib.fast()
+        ws_ptr = ws.data_ptr() if ws is not None else None
         if fp8:
-            st = lib.kvh_paged_attention_fp8(*head, float(k_scale), float(v_scale), dtype, *tail)
+            st = fast.paged_attention_fp8(
+                q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), *kcs, v_cache.data_ptr(), *vcs,
+                num_blocks, out.data_ptr(), out.stride(0), out.stride(1), tables.data_ptr(), tables.stride(0), width,
+                seq_lens.data_ptr(), qsl.data_ptr(), num_tokens, num_seqs, num_heads, num_kv_heads, head_dim,
+                block_size, max_q, float(scale), float(k_scale), float(v_scale), dtype, ws_ptr, ws_bytes,
+                _stream_handle(q.device),
+            )  # fmt: skip
             _lib.check(st, "kvh_paged_attention_fp8")
         else:
-            st = lib.kvh_paged_attention(*head, dtype, *tail)
+            st = fast.paged_attention(
+                q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), *kcs, v_cache.data_ptr(), *vcs,
+                num_blocks, out.data_ptr(), out.stride(0), out.stride(1), tables.data_ptr(), tables.stride(0), width,
+                seq_lens.data_ptr(), qsl.data_ptr(), num_tokens, num_seqs, num_heads, num_kv_heads, head_dim,
+                block_size, max_q, float(scale), dtype, ws_ptr, ws_bytes, _stream_handle(q.device),
+            )  # fmt: skip
             _lib.check(st, "kvh_paged_attention")
         return out
 

@@ -76,6 +76,25 @@ def _run(cmd: list[str]) -> None:
         print(err, file=sys.stderr)
 
 
+def build_fastcall(verbose: bool = False) -> Path:
+    """The CPython binding of the per-step entry points (csrc/pyfast.c -> _kvhfast*.so next to
+    this file), compiled with the host compiler; it resolves libkvhip's symbols at run time."""
+    import sysconfig
+
+    out = PKG / ("_kvhfast" + sysconfig.get_config_var("EXT_SUFFIX"))
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("no C compiler for the _kvhfast binding")
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", f"-I{sysconfig.get_paths()['include']}", f"-I{INCLUDE}",
+           str(CSRC / "pyfast.c"), "-ldl", "-o", str(tmp)]  # fmt: skip
+    if verbose:
+        print(" ".join(cmd))
+    _run(cmd)
+    os.replace(tmp, out)
+    return out
+
+
 def build(
     verbose: bool = False, extra_flags: list[str] | None = None, out: Path | None = None, build_dir: Path | None = None
 ) -> Path:
@@ -107,6 +126,8 @@ def build(
         print(" ".join(cmd))
     _run(cmd)
     os.replace(tmp, lib)  # atomic: a process that already mapped the old file keeps it
+    if out is None:
+        build_fastcall(verbose)
     return lib
 
 

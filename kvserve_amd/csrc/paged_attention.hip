@@ -2074,8 +2074,16 @@ static int launch_decode_nt(PAParams& p, hipStream_t s) {
   const int plan_wgs = p.PLAN ? 1 : 0;  // workgroup 0 plans the prefill launch
   int waves = (resident_blocks(k) - plan_wgs) * kWavesPerWG;
   if (waves > kMaxDecodeWaves) waves = kMaxDecodeWaves;
-  if (waves < kWavesPerWG) waves = kWavesPerWG;
-  p.NU = waves / p.HGW;
+  int64_t units = waves / p.HGW;
+  // No launch takes more units than its static shape can give work (kMinUnitChunks chunks of
+  // at most W BS keys per segment): a small batch dispatches a grid of its own size, and the
+  // merge launch scans that many job records, not one per wave the device could hold.
+  const int64_t seg_chunks = ((int64_t)p.W * p.BS + kChunk - 1) / kChunk;
+  const int64_t max_chunks = (int64_t)(p.Hkv / p.HGW) * p.B * (seg_chunks > 1 ? seg_chunks : 1);
+  const int64_t cap = (max_chunks + kMinUnitChunks - 1) / kMinUnitChunks;
+  if (units > cap) units = cap;
+  if (units < 1) units = 1;
+  p.NU = (int32_t)units;
   const int wgs = (p.NU * p.HGW + kWavesPerWG - 1) / kWavesPerWG;
   hipLaunchKernelGGL((pa_decode_kernel<E, D, NT, KV8>), dim3(wgs + plan_wgs), dim3(256), 0, s, p);
   return (int)hipGetLastError();

@@ -253,9 +253,7 @@ __device__ __forceinline__ void rope_pair_out(const GemvRopeArgs& a, int row, in
 
 template <int DT, int M, bool KV8>
 __global__ __launch_bounds__(256) void gemv_rope_cache_kernel(GemvRopeArgs a) {
-  using R = RopeElem<DT>;
   using E = std::conditional_t<DT == 2, BF16, F16>;
-  constexpr int CB = KV8 ? 1 : 2;  // bytes per cache element
   const int lane = threadIdx.x & 63;
   const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int half = a.D / 2;

@@ -86,6 +86,34 @@ def _call(lib, a):
 )
 def test_attention_validation(lib, over, status):
     assert _call(lib, _attn_args(**over)) == status
+    assert _call_fast(_attn_args(**over)) == status
+
+
+def _call_fast(a):
+    """The same call through the METH_FASTCALL binding the backend uses per step."""
+    return _lib.fast().paged_attention(
+        a["q"], a["q_ts"], a["q_hs"], a["kc"], *a["kcs"], a["vc"], *a["vcs"], a["nb"],
+        a["out"], a["o_ts"], a["o_hs"], a["bt"], a["bt_rs"], a["W"], a["sl"], a["qsl"], a["T"], a["B"], a["H"],
+        a["Hkv"], a["D"], a["BS"], a["max_q"], a["scale"], a["dtype"], a["ws"] or None, a["ws_bytes"], a["stream"],
+    )  # fmt: skip
+
+
+def test_fast_binding_is_bound_to_the_loaded_library(lib):
+    """_kvhfast resolves its entry points in the library ctypes opened; argument count and
+    type errors are Python exceptions, statuses come back unchanged."""
+    fast = _lib.fast()
+    with pytest.raises(TypeError, match="32 arguments"):
+        fast.paged_attention(1, 2)
+    with pytest.raises(TypeError):
+        fast.paged_attention(*(["x"] * 32))
+    strides = (16 * 8 * 128, 8 * 128, 128)
+    args = [0x1000, 8 * 128, 128, 0x2000, 8 * 128, 128, 0x3000, *strides, 0x4000, *strides, 0x5000, 10, 100, 8, 128, 16]
+    assert fast.reshape_and_cache(*args, 9, None) == E_DTYPE
+    assert fast.reshape_and_cache_fp8(*args, 2, 0.0, 1.0, None) == E_SHAPE  # scale must be positive
+    rope = [0x1000, 48 * 128, 0x2000, 0x3000, 0x3800, 64, 0x4000, 32 * 128, 128, 0x5000, *strides, 0x6000, *strides,
+            0x7000, 10, 100, 32, 8, 128, 16]  # fmt: skip
+    assert fast.rope_and_cache(*rope, 9, 0, 1.0, 1.0, None) == E_DTYPE
+    assert fast.rope_and_cache(*rope, 2, 1, -1.0, 1.0, None) == E_SHAPE
 
 
 def test_empty_batch_is_a_no_op(lib):
@@ -190,9 +218,10 @@ def test_host_tensors_are_rejected_before_the_library(monkeypatch):
     """A CPU tensor's address must never reach a kernel: every tensor argument is checked
     against the caches' device before any library call (a GPU memory fault otherwise)."""
     monkeypatch.setattr(attention._lib, "load", lambda: _NoLib())
+    monkeypatch.setattr(attention._lib, "fast", lambda: _NoLib())
     monkeypatch.setattr(attention, "_workspace_size", lambda *a: 0)
     T, H, Hkv, D, BS, NB = 4, 8, 2, 64, 16, 8
-    layout = (NB, BS, Hkv, D, _lib.i64x3((BS * Hkv * D, Hkv * D, D)), _lib.i64x3((BS * Hkv * D, Hkv * D, D)), 0)
+    layout = (NB, BS, Hkv, D, (BS * Hkv * D, Hkv * D, D), (BS * Hkv * D, Hkv * D, D), 0)
     monkeypatch.setattr(attention, "_cache_layout", lambda kc, vc: layout)
     kc = torch.zeros(NB, BS, Hkv, D, dtype=torch.bfloat16)
     q = torch.zeros(T, H, D, dtype=torch.bfloat16)
