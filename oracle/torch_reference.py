@@ -82,33 +82,3 @@ def forward(
     assert res.shape[0] == num_tokens
     return res
 
-
-def forward_chunked(
-    q: torch.Tensor,
-    k_cache: torch.Tensor,
-    v_cache: torch.Tensor,
-    block_tables: torch.Tensor,
-    seq_lens: torch.Tensor,
-    query_lens: torch.Tensor,
-    scale: float,
-    seqs_per_chunk: int = 1,
-    seq_ids: list[int] | None = None,
-) -> tuple[torch.Tensor, list[int]]:
-    """forward() over groups of sequences (attention is independent per sequence, so the
-    result is unchanged) to bound the padded [B, H, S, D] intermediates. Returns the
-    concatenated rows of the chosen sequences and their flat token indices."""
-    ql = [int(x) for x in query_lens.tolist()]
-    starts = [0]
-    for n in ql:
-        starts.append(starts[-1] + n)
-    ids = list(range(len(ql))) if seq_ids is None else list(seq_ids)
-    outs, rows = [], []
-    for c0 in range(0, len(ids), seqs_per_chunk):
-        grp = ids[c0 : c0 + seqs_per_chunk]
-        tok = [t for s in grp for t in range(starts[s], starts[s + 1])]
-        sub_q = q[tok]
-        width = -(-int(seq_lens[grp].max()) // k_cache.shape[1])
-        o = forward(sub_q, k_cache, v_cache, block_tables[grp][:, :width], seq_lens[grp], query_lens[grp], scale)
-        outs.append(o)
-        rows += tok
-    return torch.cat(outs), rows

@@ -303,3 +303,22 @@ def test_wide_gqa_groups(hip_device, heads, q_lens, ctx_lens, dtype):
     assert torch.isfinite(out.float()).all()
     err = (out.float().cpu() - pc.torch_oracle_full(b)).abs().max().item()
     assert err <= pc.TOL_16BIT, f"{heads} {q_lens}: {err} ({last_launch_kernels()})"
+
+
+def test_auto_selector_on_the_device(hip_device):
+    """The selector on a real gfx950 device, nothing patched: "auto" gives HipAttention for
+    block sizes the 16-token tiles divide and the caller's fallback otherwise (the reference's
+    contract, src/kvserve/attention.py:113-124); "hip" raises for a block size it cannot tile."""
+    from kvserve_amd import get_backend, hip_eligible
+
+    fallback = object()
+    for bs in (16, 32, 64):
+        assert hip_eligible(hip_device, bs)
+        assert get_backend("auto", hip_device, bs, fallback) is HipAttention
+        assert get_backend("hip", hip_device, bs) is HipAttention
+    for bs in (8, 24):
+        assert get_backend("auto", hip_device, bs, fallback) is fallback
+        with pytest.raises(ValueError):
+            get_backend("hip", hip_device, bs)
+    assert get_backend("auto", "cpu", 16, fallback) is fallback
+    assert get_backend("auto", hip_device, 8) is None
