@@ -2079,9 +2079,14 @@ static int launch_decode_nt(PAParams& p, hipStream_t s) {
   // unit (RS x D per wave), written here and read back by the merge; with half the units the
   // pieces are twice as long and the partial traffic halves, while 4 waves per SIMD still
   // keep HBM busy (measured HBM-cold, C2 5.46 -> 5.62 TB/s, C5 3.88 -> 4.20 TB/s; a quarter
-  // of the waves loses 10-20%). E4M3 caches convert every element before the MFMA and need
-  // the full wave count to hide that (4.62 -> 4.37 TB/s at half).
-  if (!KV8) units /= 2;
+  // of the waves loses 10-20%). E4M3 caches convert every element before the MFMA and keep
+  // two thirds (2 of the 3 waves per SIMD the kernel fits): with three, the last-dispatched
+  // workgroups of each CU finish up to 50% later than the first (HBM-cold C2 2%, C4 4% slower
+  // than with two), while half the waves is 5% slower.
+  if (!KV8)
+    units /= 2;
+  else
+    units = units * 2 / 3;
   // No launch takes more units than its static shape can give work (kMinUnitChunks chunks of
   // at most W BS keys per segment): a small batch dispatches a grid of its own size, and the
   // merge launch scans that many job records, not one per wave the device could hold.
