@@ -9,7 +9,7 @@ import dataclasses
 import pytest
 import torch
 
-from kvserve_amd import HipAttention
+from kvserve_amd import HipAttention, _lib
 from kvserve_amd.engine import LLAMA_3_2_1B
 from tests.engine_backends import rope as rope_table
 from oracle import torch_reference
@@ -94,9 +94,9 @@ def test_argument_errors(hip_device):
 def test_gemv_rope_and_cache_is_gemv_then_rope_and_cache(hip_device, dtype, m, H, Hkv, D, k, fp8):
     """The fused kernel gives the bits of the projection on kvh_gemv (m <= 4) or kvh_gemm_skinny
     (m > 4) followed by rope_and_cache: the same q, the same cache bytes (16-bit or E4M3 with
-    scales), slots outside the pool skipped; k = 136 runs the GEMV's tail loop."""
-    if m > 4 and k % 1024:
-        pytest.skip("the MFMA form takes k % 1024 == 0")
+    scales), slots outside the pool skipped; k = 136 runs the GEMV's tail loop. Past 4 rows with
+    k % 1024 != 0 (no MFMA form) the library rejects the call before any launch and the caches
+    stay untouched."""
     from kvserve_amd.engine import ops
     from oracle import fp8 as fp8_oracle
 
@@ -115,6 +115,14 @@ def test_gemv_rope_and_cache_is_gemv_then_rope_and_cache(hip_device, dtype, m, H
     if fp8:
         kc, vc = fp8_oracle.quantize(kc, 1.0).to(hip_device), fp8_oracle.quantize(vc, 1.0).to(hip_device)
     kc2, vc2 = kc.clone(), vc.clone()
+    if m > 4 and k % 1024:
+        with pytest.raises(_lib.KvhError) as err:
+            HipAttention.gemv_rope_and_cache(x, w, pos, rope.cos, rope.sin, kc, vc, slots, H, **sc)
+        assert err.value.status == -5  # KVH_E_UNSUPPORTED
+        torch.cuda.synchronize()
+        assert torch.equal(kc.view(torch.uint8), kc2.view(torch.uint8))
+        assert torch.equal(vc.view(torch.uint8), vc2.view(torch.uint8))
+        return
     got = HipAttention.gemv_rope_and_cache(x, w, pos, rope.cos, rope.sin, kc, vc, slots, H, **sc)
     proj = ops.gemv(x, w) if m <= 4 else ops.gemm_skinny(x, w)
     want = HipAttention.rope_and_cache(proj, pos, rope.cos, rope.sin, kc2, vc2, slots, H, **sc)
