@@ -20,13 +20,14 @@
 //    the K/V address path. K of the next chunk is issued as soon as the scores are done
 //    and V of the next chunk as soon as P.V is done: loads overlap compute without a
 //    second register buffer.
-//  * Decode class (q_len <= QS): stream-K. The launch keeps exactly as many waves as the GPU
-//    holds resident; the decode work of all sequences is one flat space of 32-token chunks
+//  * Decode class (q_len <= QS): stream-K. The launch takes a fixed share of the waves the GPU
+//    holds resident (all of them resident at once, never more than the static shape can
+//    give work); the decode work of all sequences is one flat space of 32-token chunks
 //    that is cut into equal contiguous ranges, one per work unit of up to 8 waves (adjacent
 //    kv heads of the same rows: a token's 8 heads are one contiguous 2 KB row at D = 128).
-//    No wave idles in a tail and each pays one start-up; a sequence split between units
-//    leaves partials that the merge kernel combines with a log-sum-exp. The split is
-//    computed on the device from seq_lens (no host sync).
+//    Each wave pays one start-up; a sequence split between units leaves partials that the
+//    merge kernel combines with a log-sum-exp. The split is computed on the device from
+//    seq_lens (no host sync).
 //  * Prefill class (q_len > QS): stream-K as well, over (sequence, kv head, 128-row tile,
 //    chunk); a workgroup of 4 waves shares each K/V chunk through an LDS ring filled by
 //    direct global->LDS loads, each wave computing 32 query rows.
