@@ -177,6 +177,40 @@ def test_decode_graph_replays_match_eager_steps(hip_device, dtype):
     assert runners[0].paths["decode_graph"] == 6
 
 
+def test_graph_padding_never_touches_allocated_blocks(hip_device):
+    """A decode step of 3 sequences replayed from the 4-row graph (one padding row): every
+    pool byte outside the scratch block and the 3 new tokens' slots is unchanged, in every
+    layer (the reference's padding check, tests/test_cuda_graph.py:86-95)."""
+    r = _runner(HipAttention, torch.float32, max_graph_batch=4, piecewise_graphs=False, num_blocks=64)
+    seqs = [Sequence(list(p)) for p in PROMPTS[:3]]
+    r.prefill(seqs)
+    before = r.kv_caches.clone()
+    bs = r.block_size
+    pos = [s.computed for s in seqs]  # the position each sequence's step writes
+    r.decode(seqs)
+    new = [(s.table[q // bs], q % bs) for s, q in zip(seqs, pos)]
+    assert r.paths["decode_graph"] == 1, r.paths
+    after = r.kv_caches
+    keep = torch.ones(after.shape[2:4], dtype=torch.bool)  # [blocks + 1, BS]
+    keep[r.pool.scratch_block] = False
+    for blk, off in new:
+        keep[blk, off] = False
+    keep = keep.to(after.device)
+    assert torch.equal(after[:, :, keep], before[:, :, keep])
+    for blk, off in new:  # the new rows were written (in every layer)
+        assert not torch.equal(after[:, :, blk, off], before[:, :, blk, off])
+
+
+def test_batched_generation_equals_one_sequence_at_a_time(hip_device):
+    """fp32 greedy tokens of four prompts generated together (mixed prefill / decode steps,
+    both graph modes) equal those of each prompt generated alone (the reference's batched vs
+    single check, tests/test_engine.py:46-94)."""
+    together = generate(_runner(HipAttention, torch.float32, max_graph_batch=8, token_budget=64), PROMPTS, 12)
+    alone = [generate(_runner(HipAttention, torch.float32, max_graph_batch=8, token_budget=64), [p], 12)[0]
+             for p in PROMPTS]  # fmt: skip
+    assert together == alone
+
+
 def test_bf16_llama_1b_shape_tracks_the_torch_backend(hip_device):
     """The Llama-3.2-1B layer shapes (32 q / 8 kv heads, D 64) in bf16 with two layers, a
     48-token budget so prompts are chunked into mixed steps, graphs on: teacher-forced against
