@@ -322,3 +322,48 @@ def test_auto_selector_on_the_device(hip_device):
             get_backend("hip", hip_device, bs)
     assert get_backend("auto", "cpu", 16, fallback) is fallback
     assert get_backend("auto", hip_device, 8) is None
+
+
+@pytest.mark.parametrize("layout", ["padded_rows", "head_major"])
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "e4m3"])
+def test_strided_cache_layouts(hip_device, layout, fp8):
+    """Caches as views with non-packed strides -- rows padded past head_dim (NaN in the
+    padding), or a head-major pool [blocks, heads, slots, D] seen as [blocks, slots, heads, D]
+    -- through write_kv and a forward with decode rows and prefill tiles: the same bits as the
+    same calls on packed caches (the launch plan depends on shapes only), and the packed run
+    within tolerance of the fp64 oracle."""
+    H, Hkv, D, BS = 32, 8, 128, 16
+    w = workloads.custom("strided_cache", [1, 1, 3, 70], [300, 40, 100, 33], H, Hkv, D, BS, seed=5)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=5)
+    NB = b.k_cache.shape[0]
+    kw = {}
+    kc, vc = b.k_cache, b.v_cache
+    if fp8:
+        kw = {"k_scale": 0.5, "v_scale": 0.25}
+        kc = (kc.float() / 0.5).clamp(-448, 448).to(torch.float8_e4m3fn)
+        vc = (vc.float() / 0.25).clamp(-448, 448).to(torch.float8_e4m3fn)
+
+    def strided_copy(c):
+        if layout == "padded_rows":
+            big = torch.empty((NB, BS, Hkv, D + 64), dtype=c.dtype, device=c.device)
+            big.view(torch.uint8).fill_(0x7F if fp8 else 0xFF)  # NaN in E4M3 / bf16
+            view = big[..., :D]
+        else:
+            view = torch.empty((NB, Hkv, BS, D), dtype=c.dtype, device=c.device).permute(0, 2, 1, 3)
+        view.copy_(c)
+        assert not view.is_contiguous() and view.shape == c.shape
+        return view
+
+    ks, vs = strided_copy(kc), strided_copy(vc)
+    bits = torch.uint8 if fp8 else torch.int16
+    for k_cache, v_cache in ((kc, vc), (ks, vs)):
+        HipAttention.write_kv(k_cache, v_cache, b.k_new, b.v_new, b.meta.slot_mapping, **kw)
+    assert torch.equal(ks.contiguous().view(bits), kc.view(bits))
+    assert torch.equal(vs.contiguous().view(bits), vc.view(bits))
+    ref = HipAttention.forward(b.q, kc, vc, b.meta, w.scale, **kw)
+    got = HipAttention.forward(b.q, ks, vs, b.meta, w.scale, **kw)
+    torch.cuda.synchronize()
+    assert "prefill" in last_launch_kernels()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    if not fp8:  # E4M3 attention against the oracle: tests/test_hip_fp8.py
+        assert pc.max_err_vs_oracle(b, ref, list(range(len(w.query_lens)))) <= pc.TOL_16BIT
