@@ -124,6 +124,26 @@ def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0, f
     torch.cuda.synchronize()
     ms_step = start.elapsed_time(end) / steps
 
+    # the same step replayed from a HIP graph (as a serving engine's decode runs it): the GPU
+    # time of the step without the host's per-call launch path
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        step()
+    graph.replay()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms_step_graph = start.elapsed_time(end) / steps
+    del graph
+
     # HBM-cold timings: a 1 GiB read before each timed call evicts the 256 MB Infinity Cache
     # and the L2s (the reference flushes 256 MB for a 72 MB L2, bench/bench_kernel.py:36). A
     # read, not a write: written lines would stay dirty in the caches and their write-back
@@ -166,6 +186,7 @@ def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0, f
         "step_gbs": step_bytes / (ms_step * 1e-3) / 1e9,
         "ms_per_step_cold": ms_step_cold,
         "step_gbs_cold": step_bytes / (ms_step_cold * 1e-3) / 1e9,
+        "ms_per_step_graph": ms_step_graph,
         "attn_bytes": attn_bytes,
         "kernel_ms": kernel_ms,
         "kernels": kinds,
