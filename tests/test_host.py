@@ -407,3 +407,17 @@ def test_gemm_skinny_silu_mul_validation(lib, over, status):
     st = lib.kvh_gemm_skinny_silu_mul(a["x"], a["xs"], a["w"], a["ws"], a["y"], a["ys"], a["m"], a["n"], a["k"],
                                       a["dtype"], None)  # fmt: skip
     assert st == status
+
+
+def test_bench_refuses_more_than_one_gpu_and_a_missing_gpu():
+    """bench.py measures one GPU: --gpus 2 exits with status 2 and says so; without a GPU it
+    exits with status 1 instead of measuring anything on the host."""
+    import subprocess
+    import sys
+
+    bench = str(ROOT / "bench.py")
+    r = subprocess.run([sys.executable, bench, "--gpus", "2"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2 and "one GPU" in r.stderr and not r.stdout.strip()
+    if not torch.cuda.is_available():
+        r = subprocess.run([sys.executable, bench, "--only", "1"], capture_output=True, text=True, timeout=300)
+        assert r.returncode == 1 and "needs a ROCm GPU" in r.stderr and not r.stdout.strip()
