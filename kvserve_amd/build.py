@@ -4,6 +4,9 @@
 
 Objects go to kvserve_amd/_build/, the library to kvserve_amd/lib/. Both are git-ignored
 build products; the library travels with the source tree so a GPU host needs no compiler.
+Every source's device code is also compiled to assembly (same flags) and checked for spill
+stores the compiler placed where part of the wave is disabled (kvserve_amd/isa_check.py); a
+library with one is not linked.
 """
 
 from __future__ import annotations
@@ -14,6 +17,12 @@ import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
+
+if __package__:
+    from kvserve_amd import isa_check
+else:  # run as a script
+    sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
+    from kvserve_amd import isa_check
 
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
@@ -68,8 +77,9 @@ def hipcc() -> str:
 
 def _run(cmd: list[str]) -> None:
     res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(line for line in (res.stdout + res.stderr).splitlines() if noise not in line)
+    # the host pass does not know the packed-fp32 feature; hipcc adds --hip-link to -S runs too
+    noise = ("is not a recognized feature for this target", "argument unused during compilation: '--hip-link'")
+    err = "\n".join(line for line in (res.stdout + res.stderr).splitlines() if not any(n in line for n in noise))
     if res.returncode != 0:
         raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{err}")
     if err.strip():
@@ -117,9 +127,28 @@ def build(
         _run(cmd)
         return obj
 
-    jobs = min(len(SOURCES), int(os.environ.get("MAX_JOBS", "8")), 16)
+    def assemble_one(src: str) -> Path:
+        # the same device compilation as compile_one, stopped at the assembly
+        asm = objdir / (Path(src).stem + ".gfx950.s")
+        cmd = [cc, *flags, *SOURCE_FLAGS.get(src, []), f"-I{INCLUDE}", "--cuda-device-only", "-S", str(CSRC / src),
+               "-o", str(asm)]  # fmt: skip
+        _run(cmd)
+        return asm
+
+    jobs = min(2 * len(SOURCES), int(os.environ.get("MAX_JOBS", "8")), 16)
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(compile_one, SOURCES))
+        # the two slowest compilations (paged_attention's object and assembly) start first
+        order = sorted(SOURCES, key=lambda s: s != "paged_attention.hip")
+        asm_futs = {s: ex.submit(assemble_one, s) for s in order}
+        obj_futs = {s: ex.submit(compile_one, s) for s in order}
+        objs = [obj_futs[s].result() for s in SOURCES]
+        asms = [asm_futs[s].result() for s in SOURCES]
+    bad = [f"{asm.name}: {hit}" for asm in asms for hit in isa_check.check(asm.read_text())]
+    if bad:
+        raise RuntimeError(
+            "the compiler placed spill stores where some lanes are disabled (their reloads would hand those "
+            "lanes stale values); change the kernel's register pressure or branch structure:\n" + "\n".join(bad)
+        )
     tmp = lib.with_suffix(".so.tmp")
     cmd = [cc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     if verbose:

@@ -421,3 +421,72 @@ def test_bench_refuses_more_than_one_gpu_and_a_missing_gpu():
     if not torch.cuda.is_available():
         r = subprocess.run([sys.executable, bench, "--only", "1"], capture_output=True, text=True, timeout=300)
         assert r.returncode == 1 and "needs a ROCm GPU" in r.stderr and not r.stdout.strip()
+
+
+# A kernel shaped like the page-table load of the prefill kernel: a divergent load, then the
+# join. SPILL marks where the register allocator put the spill store of a live-everywhere pair.
+_ISA_TEMPLATE = """_ZN3kvh4testEv:
+; %bb.0:
+\tv_cmp_gt_i32_e32 vcc, s5, v0
+\ts_and_saveexec_b64 s[8:9], vcc
+\ts_cbranch_execz .LBB0_2
+; %bb.1:
+\tglobal_load_dwordx2 v[4:5], v[4:5], off
+{inside}
+.LBB0_2:
+{before}
+\ts_or_b64 exec, exec, s[8:9]
+{after}
+\ts_cmp_lt_i32 s6, 2
+\ts_cbranch_scc1 .LBB0_4
+; %bb.3:
+\ts_mov_b64 s[2:3], exec
+\ts_and_b64 exec, exec, s[10:11]
+{masked}
+\ts_mov_b64 exec, s[2:3]
+.LBB0_4:
+{end}
+\ts_endpgm
+.Lfunc_end0:
+"""
+
+
+def _isa(**kw):
+    slots = {k: "" for k in ("inside", "before", "after", "masked", "end")}
+    slots.update(kw)
+    return _ISA_TEMPLATE.format(**slots)
+
+
+SPILL = "\tscratch_store_dwordx2 off, v[42:43], off offset:20"
+RELOAD = "\tscratch_load_dwordx2 v[42:43], off, off offset:20"
+
+
+def test_isa_check_finds_spill_stores_under_a_partial_exec_mask():
+    from kvserve_amd import isa_check
+
+    assert isa_check.check(_isa(after=SPILL, end=SPILL + "\n" + RELOAD)) == []
+    # the faulting shape: the store in the join block ahead of the exec restore
+    (hit,) = isa_check.check(_isa(before=SPILL, end=RELOAD))
+    assert "scratch_store_dwordx2" in hit and "partial EXEC" in hit
+    assert len(isa_check.check(_isa(inside=SPILL))) == 1
+    assert len(isa_check.check(_isa(masked=SPILL))) == 1
+    # reloads inside a divergent region refill the lanes that use them: not reported
+    assert isa_check.check(_isa(inside=RELOAD, masked=RELOAD)) == []
+
+
+def test_isa_check_joins_take_the_weaker_state():
+    from kvserve_amd import isa_check
+
+    # one predecessor of the join restores EXEC, the other arrives with the narrowed mask
+    asm = _isa(end=SPILL).replace("\ts_mov_b64 exec, s[2:3]\n", "\ts_cbranch_vccz .LBB0_4\n\ts_mov_b64 exec, s[2:3]\n")
+    assert len(isa_check.check(asm)) == 1
+    assert isa_check.check(_isa(end=SPILL)) == []
+
+
+def test_built_kernels_have_no_partial_exec_spills():
+    from kvserve_amd import isa_check
+
+    asms = sorted((Path(__file__).resolve().parents[1] / "kvserve_amd" / "_build").glob("*.gfx950.s"))
+    if not asms:
+        pytest.skip("no device assembly: run python -m kvserve_amd.build")
+    assert [hit for a in asms for hit in isa_check.check(a.read_text())] == []
