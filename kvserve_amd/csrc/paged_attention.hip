@@ -240,6 +240,7 @@ struct WaveState {
   float m[NT], l[NT];     // m: running max (exp2 domain, -inf when empty); l: lane-partial sum
   int limit[NT];          // keys visible to this lane's row (0 for padding rows)
   float thr[NT], nsh[NT]; // prefill only: raw-score bound that moves m, and -m (0 while m = -inf)
+  f32x4 cinit[NT];        // prefill over pre-scaled Q only: -m in every slot, the QK accumulators' start
 };
 
 // Q rows of tile t: global row r = row0 + 16t + n, valid when r < R.
@@ -400,6 +401,76 @@ __device__ __forceinline__ void pf_lanemax(const f32x4 st[NT][2], float mx[NT]) 
   for (int t = 0; t < NT; ++t)
     mx[t] = fmaxf(fmaxf(fmaxf(st[t][0][0], st[t][0][1]), fmaxf(st[t][0][2], st[t][0][3])),
                   fmaxf(fmaxf(st[t][1][0], st[t][1][1]), fmaxf(st[t][1][2], st[t][1][3])));
+}
+
+// Whether the prefill kernel pre-scales Q: bf16 keeps fp32's exponent range, so q * scale *
+// log2(e) rounded to bf16 cannot overflow (fp16 could, so it keeps the per-score FMA).
+template <class E>
+constexpr bool kPrescaleQ = std::is_same_v<E, BF16>;
+
+// Q of a prefill wave multiplied by scale * log2(e) (sign included) and rounded to E (round to
+// nearest even), so that with accumulators started at -m the QK MFMAs hand back the exp2
+// argument x = q.k scale log2(e) - m itself; the shift starts at 0 with the row empty.
+template <class E, int D, int NT>
+__device__ __forceinline__ void pf_prescale_q(WaveState<D, NT>& s, float cs) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int cc = 0; cc < D / 32; ++cc)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t x = s.q[t][cc][w];
+        s.q[t][cc][w] = E::pack2(__uint_as_float(x << 16) * cs, __uint_as_float(x & 0xffff0000u) * cs);
+      }
+    s.m[t] = 0.f;
+    s.cinit[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+// Online-softmax update over pre-scaled Q: st holds x = (scaled score) - m, per-lane maxima of
+// x in mxs. thr is kRescaleSlack, or -inf while the row has seen no key (m = 0 then). When
+// some row of the tile passes it (a uniform branch), each row moves its shift up by its max
+// (the first visible key sets it), x and the start value -m follow, and the accumulators and
+// sums are rescaled; otherwise P = exp2(x) directly (P <= 2^kRescaleSlack).
+template <class E, int D, int NT>
+__device__ __forceinline__ void pf_softmax_pre(WaveState<D, NT>& s, f32x4 st[NT][2], const float mxs[NT],
+                                               u32x4 pt[NT]) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (__builtin_amdgcn_ballot_w64(mxs[t] > s.thr[t])) {
+      const float mrow = max_over_groups(mxs[t]);  // -inf: no visible key in this chunk
+      const bool empty = s.thr[t] == -INFINITY;
+      const bool still_empty = empty && mrow == -INFINITY;
+      const float d = still_empty ? 0.f : (empty ? mrow : fmaxf(mrow, 0.f));
+      const float alpha = empty ? 1.f : fast_exp2(-d);
+      s.l[t] *= alpha;
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) s.acc[t][i] *= alpha;
+      s.m[t] += d;
+      s.cinit[t] = f32x4{-s.m[t], -s.m[t], -s.m[t], -s.m[t]};
+      s.thr[t] = still_empty ? -INFINITY : kRescaleSlack;
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile) st[t][tile] -= d;
+    }
+    float pv[8];
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pv[4 * tile + e] = fast_exp2(st[t][tile][e]);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      pt[t][w] = E::pack2(pv[2 * w], pv[2 * w + 1]);
+      s.l[t] = E::dot2_ones(pt[t][w], s.l[t]);
+    }
+  }
+}
+
+// A row that never saw a key leaves m = -inf (the merge's empty piece), not the shift 0.
+template <int D, int NT>
+__device__ __forceinline__ void pf_prescale_finish(WaveState<D, NT>& s) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+    if (s.thr[t] == -INFINITY) s.m[t] = -INFINITY;
 }
 
 // Online-softmax update from (masked) raw scores and per-lane maxima; c > 0 so a -inf
@@ -1322,8 +1393,11 @@ __device__ __forceinline__ void pf_window(PfWindow& win, const PAParams& p, cons
     const int hh = 2 * c + h;
     const int pg = hh / r;
     off[h] = (hh - pg * r) * 16;
-    int64_t b = -1;
-    if (c < c_end && pg < page_end) b = btrow[pg];
+    // every lane loads (column 0 when its page is outside the range: W >= 1), so the load
+    // is no divergent branch whose join could hold a spill store ahead of the exec restore
+    const bool in = c < c_end && pg < page_end;
+    const int64_t raw = btrow[in ? pg : 0];
+    const int64_t b = in ? raw : -1;
     ok[h] = b >= 0 && b < p.num_blocks;
     id[h] = ok[h] ? (int)b : 0;
   }
@@ -1375,7 +1449,7 @@ __device__ __forceinline__ void pf_k_lanes(uint32_t ka[D / 32], const char* lds)
 }
 
 // S^T of one chunk from the K stage, one 16-key tile at a time (16 registers of K operands
-// live instead of 32).
+// live instead of 32). Over pre-scaled Q the accumulators start at -m (the exp2 argument).
 template <class E, int D, int NT>
 __device__ __forceinline__ void pf_scores_lds(const WaveState<D, NT>& s, const uint32_t ka[D / 32], int stage,
                                               f32x4 st[NT][2]) {
@@ -1389,7 +1463,7 @@ __device__ __forceinline__ void pf_scores_lds(const WaveState<D, NT>& s, const u
       k[cc] = *(lds_u32x4_ptr)(uintptr_t)(ka[cc] + (uint32_t)(stage + 16 * tile * L::kRowBytes));
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      f32x4 a = {0.f, 0.f, 0.f, 0.f};
+      f32x4 a = kPrescaleQ<E> ? s.cinit[t] : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int cc = 0; cc < D / 32; ++cc) a = E::mfma(k[cc], s.q[t][cc], a);
       st[t][tile] = a;
@@ -1563,10 +1637,13 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
 
   WaveState<D, NT> s;
   load_q<D, NT>(s, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
-  // The exp2 argument is fma(score, c, -m) with c > 0: for a negative scale S c = (-Q) K^T |c|
-  // (a sign flip of Q is exact), for a zero scale every score is 0 = (0 Q) K^T 1.
+  // Without pre-scaling, the exp2 argument is fma(score, c, -m) with c > 0: for a negative
+  // scale S c = (-Q) K^T |c| (a sign flip of Q is exact), for a zero scale every score is
+  // 0 = (0 Q) K^T 1.
   float c = fabsf(p.qk_scale);
-  if (p.qk_scale < 0.f) {
+  if constexpr (kPrescaleQ<E>) {
+    pf_prescale_q<E, D, NT>(s, p.qk_scale);
+  } else if (p.qk_scale < 0.f) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -1652,7 +1729,10 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
     pf_v_issue<D, SOFF + L::kTileBytes, 0, kVLead>(vt, vb);
     __builtin_amdgcn_sched_barrier(0);
     u32x4 pt[NT];
-    pf_softmax<E, D, NT>(s, sc, mx, c, pt);
+    if constexpr (kPrescaleQ<E>)
+      pf_softmax_pre<E, D, NT>(s, sc, mx, pt);
+    else
+      pf_softmax<E, D, NT>(s, sc, mx, c, pt);
     pf_pv<E, D, NT, MASKED, SOFF + L::kTileBytes>(s, vt, vb, cr, sv.kv_total, pt);
   };
   using S0 = std::integral_constant<int, 0>;
@@ -1682,6 +1762,7 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
     sync(i, next * L::kStageBytes);
     stg = stg == 2 ? 0 : stg + 1;
   }
+  if constexpr (kPrescaleQ<E>) pf_prescale_finish<D, NT>(s);
   pf_write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, slot * kPrefillRows - wg_row0);
 }
 
@@ -1714,7 +1795,9 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
   WaveState<D, NT> s;
   load_q<D, NT>(s, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
   float c = fabsf(p.qk_scale);
-  if (p.qk_scale < 0.f) {
+  if constexpr (kPrescaleQ<E>) {
+    pf_prescale_q<E, D, NT>(s, p.qk_scale);
+  } else if (p.qk_scale < 0.f) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -1817,7 +1900,10 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
     pf_v_issue<D, SOFF + L::kTileBytes, 0, kVLead>(vt, vb);
     __builtin_amdgcn_sched_barrier(0);
     u32x4 pt[NT];
-    pf_softmax<E, D, NT>(s, sc, mx, c, pt);
+    if constexpr (kPrescaleQ<E>)
+      pf_softmax_pre<E, D, NT>(s, sc, mx, pt);
+    else
+      pf_softmax<E, D, NT>(s, sc, mx, c, pt);
     pf_pv<E, D, NT, MASKED, SOFF + L::kTileBytes>(s, vt, vb, cr, sv.kv_total, pt);
   };
   using I0 = std::integral_constant<int, 0>;
@@ -1840,6 +1926,7 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
       sync(i, I0{});
     if (i < n_my) compute(i, (i & 1) * L::kStageBytes, S0{}, std::true_type{});
   }
+  if constexpr (kPrescaleQ<E>) pf_prescale_finish<D, NT>(s);
   pf_write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, slot * kPrefillRows - wg_row0);
 }
 
