@@ -1607,6 +1607,26 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Wave priority from the unit's remaining share of its work (`total` positions, `rest` of
+// them after this tile, n - i chunks of the tile left at chunk i): the arbiter favours older
+// waves, so workgroups that started together on a CU drift apart and the last one runs its
+// tail alone; raising the priority of the workgroups that are behind keeps them together.
+// The level min(3, 4 left / (total + 1)), left = rest + n - i, only falls as i grows, so it
+// is set at a tile's first chunk and again at the chunks where it drops: lvl(i) >= k exactly
+// for i <= rest + n - ceil(k (total + 1) / 4). (Checked against the per-chunk formula for
+// every total < 160, n and rest.)
+struct PfPriority {
+  int next_drop;  // first chunk whose level is below the current one
+  __device__ __forceinline__ void set(int i, int n, int rest, int total) {
+    const int lvl = min(3, (4 * (rest + n - i)) / (total + 1));
+    if (lvl >= 2)
+      lvl == 3 ? __builtin_amdgcn_s_setprio(3) : __builtin_amdgcn_s_setprio(2);
+    else
+      lvl == 1 ? __builtin_amdgcn_s_setprio(1) : __builtin_amdgcn_s_setprio(0);
+    next_drop = lvl > 0 ? rest + n - (lvl * (total + 1) + 3) / 4 + 1 : INT32_MAX;
+  }
+};
+
 // One workgroup's pass over chunks [c_lo, c_hi) of tile t of (seq, kvh): the whole tile
 // (written out) or a piece of it (partial in slot `slot` of the prefill partial arrays).
 //
@@ -1677,18 +1697,11 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
   pf_issue<D>(lds, 0, pl, win, c_lo);
   if (n > 1) pf_issue<D>(lds, L::kStageBytes, pl, win, c_lo + 1);
 
+  PfPriority prio;
+  prio.set(0, n, rest, total);
   // step i: wait for chunk i, then refill the stage chunk i - 1 used (`next`) with chunk i + 2
   auto sync = [&](int i, int next) {
-    // Wave priority from the unit's remaining share of its work (total positions, rest of
-    // them after this tile): the arbiter favours older waves, so workgroups that started
-    // together on a CU drift apart and the last one runs its tail alone; raising the
-    // priority of the workgroups that are behind keeps them together.
-    const int left = rest + (n - i);
-    const int lvl = min(3, (4 * left) / (total + 1));
-    if (lvl >= 2)
-      lvl == 3 ? __builtin_amdgcn_s_setprio(3) : __builtin_amdgcn_s_setprio(2);
-    else
-      lvl == 1 ? __builtin_amdgcn_s_setprio(1) : __builtin_amdgcn_s_setprio(0);
+    if (i >= prio.next_drop) prio.set(i, n, rest, total);
     const int ci2 = c_lo + i + 2;
     if (i + 2 < n && ci2 - win.c0 >= 64) {  // the window moves on (every 62 chunks)
       pf_window(win, p, btrow, c_lo + i, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
@@ -1843,15 +1856,12 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
   issue(raw[0], c_lo);
   if (n > 1) issue(raw[1], c_lo + 1);
 
+  PfPriority prio;  // wave priority as in prefill_tile
+  prio.set(0, n, rest, total);
   // step i: wait for chunk i's bytes, convert them into stage i % 2, publish, load chunk i + 2
   auto sync = [&](int i, auto set) {
     constexpr int S = decltype(set)::value;
-    const int left = rest + (n - i);  // wave priority as in prefill_tile
-    const int lvl = min(3, (4 * left) / (total + 1));
-    if (lvl >= 2)
-      lvl == 3 ? __builtin_amdgcn_s_setprio(3) : __builtin_amdgcn_s_setprio(2);
-    else
-      lvl == 1 ? __builtin_amdgcn_s_setprio(1) : __builtin_amdgcn_s_setprio(0);
+    if (i >= prio.next_drop) prio.set(i, n, rest, total);
     const int ci2 = c_lo + i + 2;
     if (i + 2 < n && ci2 - win.c0 >= 64) {
       pf_window(win, p, btrow, c_lo + i, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
