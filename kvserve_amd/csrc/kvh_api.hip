@@ -72,7 +72,7 @@ Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t 
     // plan: header, sequence list, flat starts, unit starts
     pl.ws_plan_bytes = pl.launch_prefill ? align_up(4 * sizeof(int64_t)) + align_up((size_t)B * sizeof(int32_t)) +
                                                align_up(((size_t)B + 1) * sizeof(int64_t)) +
-                                               align_up((size_t)kMaxPrefillUnits * 4 * sizeof(int32_t))
+                                               align_up((size_t)kMaxPrefillUnits * kPreRec * sizeof(int32_t))
                                          : 0;
     // cascade over a shared prefix: share header, decode list, prefix partials, merge jobs
     pl.cascade = !pl.launch_prefill && pl.NT == 1 && B >= 2 && (int64_t)W * BS > kCascadeMinTokens;
@@ -427,7 +427,7 @@ static int paged_attention_impl(const void* q, int64_t q_tok_stride, int64_t q_h
       p.ws_pre_beg = (int64_t*)w;
       w += align_up(((size_t)num_seqs + 1) * sizeof(int64_t));
       p.ws_pre_unit = (int32_t*)w;
-      w += align_up((size_t)kMaxPrefillUnits * 4 * sizeof(int32_t));
+      w += align_up((size_t)kMaxPrefillUnits * kPreRec * sizeof(int32_t));
     }
     if (plan.ws_x_bytes) {
       const size_t rows = (size_t)plan.xslots * plan.HGW * 16;

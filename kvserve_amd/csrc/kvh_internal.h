@@ -25,6 +25,11 @@ constexpr int32_t kCascadeMinChunks = 8;
 constexpr int32_t kShareHdr = 8;  // int64: shared tokens, prefix groups, row of the shared table, sequences
 // Merge job record: int32 fields, one record per work unit (decode units first).
 constexpr int32_t kJobInts = 16;
+// Prefill plan record: int32 fields, one 64-byte record per prefill workgroup: [0] its unit u
+// (-1: idle), [1] list index, [2] kv head, [3] tile, [4] offset within the tile, [5] sequence,
+// [6] query length, [7] kv length, and int64 pairs: [8..9] first query token, [10..11]
+// context length, [12..13] and [14..15] the flat range [x0, x1) of the unit.
+constexpr int32_t kPreRec = 16;
 constexpr int32_t kMaxJobs = kMaxDecodeWaves + kMaxPrefillUnits;
 
 // Everything a paged-attention kernel reads, by value in the kernel argument segment.
@@ -62,11 +67,11 @@ struct PAParams {
   float* ws_pacc;  // [2 NUP, PR, D] partial outputs of split prefill tiles (capacity: kPrefillRows)
   float* ws_pml;   // [2 NUP, PR, 2]
   int32_t* ws_job; // [kMaxJobs, kJobInts] merge jobs, rewritten by every unit on every call
-  // prefill plan, written by pa_plan_kernel before the prefill launch:
+  // prefill plan, written by the decode launch's workgroup 0 before any prefill unit starts:
   int64_t* ws_plan_hdr;  // [4]: flat size C, active units NUa, prefill sequences n_pre
   int32_t* ws_pre_list;  // [B] the prefill-class sequences in order
   int64_t* ws_pre_beg;   // [B + 1] flat start of each (ws_pre_beg[n_pre] = C)
-  int32_t* ws_pre_unit;  // [kMaxPrefillUnits, 4] start of unit u: list index, kv head, tile, offset
+  int32_t* ws_pre_unit;  // [kMaxPrefillUnits, kPreRec] one record per prefill workgroup
   // cascade, written by pa_share_kernel before the decode launch:
   int64_t* ws_share;     // [kShareHdr]: shared prefix tokens (multiple of 32, 0: none), groups, r0, sequences
   int32_t* ws_dec_list;  // [B] decode-class sequences in order

@@ -1299,28 +1299,39 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
 //
 // The 4 waves share every 32-key K/V chunk through a 3-stage LDS ring filled by direct
 // global->LDS loads (no VGPR staging): chunk c + 2 is in flight while chunk c is computed.
-// Each 16-byte slot s of LDS row t holds the row's global slot s ^ (t % slots_per_row), so
-// both the K-operand reads (16 rows, one slot) and the V-operand reads (4 rows, 16 slots)
-// hit 16 distinct bank groups. Waves wait with s_waitcnt on their own loads, then a bare
-// s_barrier makes all four waves' loads of the chunk visible.
+// K rows are stored in groups of kRowsPerLoad (one wave-wide load each): row r of a group
+// holds, in 16-byte slot s, the row's global slot s ^ r, and each group after the first
+// starts kKPad bytes further on, so the K-operand reads (one slot of 16 consecutive rows)
+// hit 16 distinct bank groups while the swizzle of a load does not depend on which group it
+// fills: a wave's loads share one lane offset and differ by a uniform step. Waves wait with
+// s_waitcnt on their own loads, then a bare s_barrier makes all four waves' loads of the
+// chunk visible.
 template <int D>
 struct PrefillLds {
+  static_assert(D == 64 || D == 128, "prefill head sizes");
   static constexpr int kRowBytes = D * 2;                // one token row of one kv head
   static constexpr int kSlots = kRowBytes / 16;          // 16-byte slots per row
   static constexpr int kRowsPerLoad = 1024 / kRowBytes;  // rows one wave-wide load fills
   static constexpr int kTileBytes = kChunk * kRowBytes;  // K (or V) of one chunk
   static constexpr int kLoadsPerTile = kTileBytes / 1024;
   static constexpr int kLoadsPerWave = 2 * kLoadsPerTile / kWavesPerWG;  // K and V, split over 4 waves
+  // D = 64: 8-row groups already cover the 8 slots; D = 128: 4-row groups, each shifted by
+  // 4 slots from the previous (group g of a 16-row half spans bank groups 4 g + (0..3)).
+  static constexpr int kKPad = kRowsPerLoad < kSlots ? 16 * kRowsPerLoad : 0;
+  static constexpr int kKLoadBytes = 1024 + kKPad;          // one K row group
+  static constexpr int kKHalfBytes = 16 / kRowsPerLoad * kKLoadBytes;  // 16 K rows
+  static constexpr int kKBytes = kLoadsPerTile * kKLoadBytes;  // K of one chunk (V follows)
   static constexpr int kStages = 3;
-  static constexpr int kStageBytes = 2 * kTileBytes;
+  static constexpr int kStageBytes = kKBytes + kTileBytes;
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // One wave's share of the direct global->LDS loads of a chunk: kLoadsPerWave loads of
 // kRowsPerLoad rows each, all of K or all of V and all in the same 16-token half, so one
-// uniform base address per wave and chunk; the rows and swizzled slots of the loads are
-// folded into per-lane byte offsets (the loads take the SGPR base + VGPR offset form).
+// uniform base address per wave and chunk. Load k reads lane offset loff from the base plus
+// k ustep bytes (SGPR base + VGPR offset form, one offset register for all loads) into the
+// stage at dst + k lstride.
 template <int D>
 struct PfLoads {
   using L = PrefillLds<D>;
@@ -1330,7 +1341,9 @@ struct PfLoads {
   int64_t sb2, ss2;   // block and slot strides of that cache in bytes
   int h;              // the half (0: tokens 0-15 of the chunk, 1: 16-31)
   int dst;            // LDS byte offset of the first load within a stage
-  uint32_t loff[L::kLoadsPerWave];
+  int lstride;        // LDS bytes from one load to the next
+  uint32_t ustep;     // global bytes from one load to the next (wave-uniform)
+  uint32_t loff;      // the lane's global byte offset in the first load
 };
 
 // EB: bytes per cache element (2; 1 for an E4M3 cache, whose granules are the same 8
@@ -1347,24 +1360,25 @@ __device__ __forceinline__ void pf_loads_init(PfLoads<D>& pl, const PAParams& p,
   pl.ss2 = EB * (v ? p.v_ss : p.k_ss);
   pl.cache = (const char*)(v ? p.vc : p.kc) + (int64_t)kvh * (v ? p.v_sh : p.k_sh) * EB;
   pl.h = i0 * L::kRowsPerLoad / 16;
-  pl.dst = (v ? L::kTileBytes : 0) + i0 * 1024;
   if (!v) {
-#pragma unroll
-    for (int k = 0; k < L::kLoadsPerWave; ++k) {
-      const int row = (i0 + k) * L::kRowsPerLoad + row_in;  // row of the chunk (0..31)
-      pl.loff[k] = (uint32_t)((row % 16) * pl.ss2) + 8u * EB * (uint32_t)(slot ^ (row % L::kSlots));
-    }
+    // load k fills row group i0 + k: rows (i0 + k) R + row_in of the chunk, token
+    // (k R + row_in) of half h's page (R = kRowsPerLoad, k R + row_in < 16), slot s ^ row_in
+    pl.dst = i0 * L::kKLoadBytes;
+    pl.lstride = L::kKLoadBytes;
+    pl.ustep = (uint32_t)(L::kRowsPerLoad * pl.ss2);
+    pl.loff = (uint32_t)(row_in * pl.ss2) + 8u * EB * (uint32_t)(slot ^ row_in);
   } else {
     // V stage layout: blocks b = h (D/16) + i of 512 bytes, block b holding d = 16i .. 16i+15
     // of the 16 tokens of half h, token-major (32 bytes per token). 16-byte granule P of the
     // stage is token (P % 32) / 2 of the half, global 16-byte chunk 2 (b % (D/16)) + P % 2.
+    // Load k is granules P = 64 (i0 + k) + lane: the same token, chunk 4 k further on
+    // (b % (D/16) = 2 k + lane / 32, since i0 is 0 or half the loads of a tile).
     pl.h = 2 * i0 / (D / 16);
-#pragma unroll
-    for (int k = 0; k < L::kLoadsPerWave; ++k) {
-      const int P = 64 * (i0 + k) + lane;
-      const int b = P / 32, tok = (P % 32) / 2, chunk = 2 * (b % (D / 16)) + P % 2;
-      pl.loff[k] = (uint32_t)(tok * pl.ss2) + 8u * EB * (uint32_t)chunk;
-    }
+    const int b = (64 * i0 + lane) / 32, tok = (lane % 32) / 2, chunk = 2 * (b % (D / 16)) + lane % 2;
+    pl.dst = L::kKBytes + i0 * 1024;
+    pl.lstride = 1024;
+    pl.ustep = 32u * EB;
+    pl.loff = (uint32_t)(tok * pl.ss2) + 8u * EB * (uint32_t)chunk;
   }
 }
 
@@ -1424,14 +1438,14 @@ __device__ __forceinline__ void pf_issue(char* lds, int stage, const PfLoads<D>&
   const int rel = ci - win.c0;
   const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(win.off_hi, rel) << 32) |
                      (uint32_t)__builtin_amdgcn_readlane(win.off_lo, rel);
-  uint64_t base = (uint64_t)(uintptr_t)pl.cache + o;
-  asm volatile("" : "+s"(base));
+  uint32_t off = pl.loff;
+  asm volatile("" : "+v"(off));  // a 32-bit offset in this block: the loads' VGPR operand
 #pragma unroll
   for (int k = 0; k < L::kLoadsPerWave; ++k) {
-    uint32_t off = pl.loff[k];
-    asm volatile("" : "+v"(off));  // a 32-bit offset in this block: the load's VGPR operand
+    uint64_t base = (uint64_t)(uintptr_t)pl.cache + o + (uint64_t)k * pl.ustep;
+    asm volatile("" : "+s"(base));
     __builtin_amdgcn_global_load_lds((const void*)((const char*)(uintptr_t)base + off),
-                                     (lds_ptr_t)(lds + stage + pl.dst + k * 1024), 16, 0, 0);
+                                     (lds_ptr_t)(lds + stage + pl.dst + k * pl.lstride), 16, 0, 0);
   }
 }
 
@@ -1444,8 +1458,9 @@ __device__ __forceinline__ void pf_k_lanes(uint32_t ka[D / 32], const char* lds)
   const int j = lane >> 4, n = lane & 15;
 #pragma unroll
   for (int cc = 0; cc < D / 32; ++cc)
-    ka[cc] = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds + n * L::kRowBytes +
-             16 * ((4 * cc + j) ^ (n % L::kSlots));
+    ka[cc] = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds +
+             n / L::kRowsPerLoad * L::kKLoadBytes + n % L::kRowsPerLoad * L::kRowBytes +
+             16 * ((4 * cc + j) ^ (n % L::kRowsPerLoad));
 }
 
 // S^T of one chunk from the K stage, one 16-key tile at a time (16 registers of K operands
@@ -1460,7 +1475,7 @@ __device__ __forceinline__ void pf_scores_lds(const WaveState<D, NT>& s, const u
     u32x4 k[D / 32];
 #pragma unroll
     for (int cc = 0; cc < D / 32; ++cc)
-      k[cc] = *(lds_u32x4_ptr)(uintptr_t)(ka[cc] + (uint32_t)(stage + 16 * tile * L::kRowBytes));
+      k[cc] = *(lds_u32x4_ptr)(uintptr_t)(ka[cc] + (uint32_t)(stage + tile * L::kKHalfBytes));
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       f32x4 a = kPrescaleQ<E> ? s.cinit[t] : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1739,14 +1754,14 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
     __builtin_amdgcn_sched_barrier(0);
     VTr<D> vt;
     const uint32_t vb = vbase + (uint32_t)stage;
-    pf_v_issue<D, SOFF + L::kTileBytes, 0, kVLead>(vt, vb);
+    pf_v_issue<D, SOFF + L::kKBytes, 0, kVLead>(vt, vb);
     __builtin_amdgcn_sched_barrier(0);
     u32x4 pt[NT];
     if constexpr (kPrescaleQ<E>)
       pf_softmax_pre<E, D, NT>(s, sc, mx, pt);
     else
       pf_softmax<E, D, NT>(s, sc, mx, c, pt);
-    pf_pv<E, D, NT, MASKED, SOFF + L::kTileBytes>(s, vt, vb, cr, sv.kv_total, pt);
+    pf_pv<E, D, NT, MASKED, SOFF + L::kKBytes>(s, vt, vb, cr, sv.kv_total, pt);
   };
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, L::kStageBytes>;
@@ -1844,12 +1859,12 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
     const int rel = ci - win.c0;
     const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(win.off_hi, rel) << 32) |
                        (uint32_t)__builtin_amdgcn_readlane(win.off_lo, rel);
-    uint64_t base = (uint64_t)(uintptr_t)pl.cache + o;
-    asm volatile("" : "+s"(base));
+    uint32_t off = pl.loff;
+    asm volatile("" : "+v"(off));
 #pragma unroll
     for (int k = 0; k < KLW; ++k) {
-      uint32_t off = pl.loff[k];
-      asm volatile("" : "+v"(off));
+      uint64_t base = (uint64_t)(uintptr_t)pl.cache + o + (uint64_t)k * pl.ustep;
+      asm volatile("" : "+s"(base));
       r[k] = *(const u32x2*)((const char*)(uintptr_t)base + off);
     }
   };
@@ -1879,7 +1894,7 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
       const u32x4 o = {E::template from_fp8x2<false>(r[0]), E::template from_fp8x2<true>(r[0]),
                        E::template from_fp8x2<false>(r[1]), E::template from_fp8x2<true>(r[1])};
       *(lds_u32x4_ptr)(uintptr_t)((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds +
-                                  (uint32_t)(S * L::kStageBytes + pl.dst + k * 1024 + 16 * lane)) = o;
+                                  (uint32_t)(S * L::kStageBytes + pl.dst + k * pl.lstride + 16 * lane)) = o;
     }
     __syncthreads();  // the stage's writes are complete and visible; nothing else in flight
     __builtin_amdgcn_sched_barrier(0);
@@ -1907,14 +1922,14 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
     __builtin_amdgcn_sched_barrier(0);
     VTr<D> vt;
     const uint32_t vb = vbase + (uint32_t)stage;
-    pf_v_issue<D, SOFF + L::kTileBytes, 0, kVLead>(vt, vb);
+    pf_v_issue<D, SOFF + L::kKBytes, 0, kVLead>(vt, vb);
     __builtin_amdgcn_sched_barrier(0);
     u32x4 pt[NT];
     if constexpr (kPrescaleQ<E>)
       pf_softmax_pre<E, D, NT>(s, sc, mx, pt);
     else
       pf_softmax<E, D, NT>(s, sc, mx, c, pt);
-    pf_pv<E, D, NT, MASKED, SOFF + L::kTileBytes>(s, vt, vb, cr, sv.kv_total, pt);
+    pf_pv<E, D, NT, MASKED, SOFF + L::kKBytes>(s, vt, vb, cr, sv.kv_total, pt);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -1964,10 +1979,10 @@ __device__ __forceinline__ int64_t pre_seq_chunks(const PAParams& p, const SeqVi
 
 // Prefill plan, computed by workgroup 0 of the decode launch in mixed batches (so it runs
 // under the decode work instead of ahead of it): the list of prefill-class sequences, the
-// flat start of each (prefix sums of Hkv x pre_seq_chunks) and, for each work unit u < NUa,
-// the sequence (list index), kv head, tile and position within the tile of its first flat
-// position u C / NUa. Every prefill workgroup then starts from two loads instead of
-// scanning the batch itself.
+// flat start of each (prefix sums of Hkv x pre_seq_chunks) and, for each prefill workgroup,
+// a record of where its unit starts (below). Every prefill workgroup then starts from one
+// scalar load of its record instead of scanning the batch or chasing the unit -> sequence
+// -> lengths chain through memory.
 __device__ void plan_prefill(const PAParams& p) {
   __shared__ int64_t s_pos[kPlanThreads];
   __shared__ int32_t s_cnt[kPlanThreads];
@@ -2017,7 +2032,16 @@ __device__ void plan_prefill(const PAParams& p) {
   }
   __syncthreads();  // the list and starts are visible to the whole workgroup
   const int64_t* beg_tab = n_pre <= kPlanLdsSeqs ? s_beg : p.ws_pre_beg;
-  for (int u = tid; u < NUa; u += kPlanThreads) {
+  const int q8 = NUa / 8, r8 = NUa % 8;
+  for (int b = tid; b < p.NUP; b += kPlanThreads) {
+    // workgroup b's unit, as prefill_units deals them: XCD by XCD (b % 8), then b / 8
+    const int xcd = b % 8, jj = b / 8;
+    int32_t* d = p.ws_pre_unit + (int64_t)b * kPreRec;
+    if (NUa == 0 || jj >= q8 + (xcd < r8 ? 1 : 0)) {
+      d[0] = -1;  // idle, rewritten on every call
+      continue;
+    }
+    const int u = xcd * q8 + min(xcd, r8) + jj;
     const int64_t x0 = u * C / NUa;
     int lo = 0, hi = n_pre - 1;  // last sequence starting at or before x0
     while (lo < hi) {
@@ -2027,7 +2051,8 @@ __device__ void plan_prefill(const PAParams& p) {
       else
         hi = mid - 1;
     }
-    const SeqView sv = seq_view(p, p.ws_pre_list[lo]);
+    const int seq = p.ws_pre_list[lo];
+    const SeqView sv = seq_view(p, seq);
     const int R = sv.q_len * p.G;
     const int64_t per_kvh = (beg_tab[lo + 1] - beg_tab[lo]) / p.Hkv;
     const int64_t off = x0 - beg_tab[lo];
@@ -2038,11 +2063,19 @@ __device__ void plan_prefill(const PAParams& p) {
       rem -= kTileCost + n_t;
       ++t;
     }
-    int32_t* d = p.ws_pre_unit + (int64_t)u * 4;
-    d[0] = lo;
-    d[1] = kvh;
-    d[2] = t;
-    d[3] = (int)rem;  // < kTileCost + chunks of one tile
+    const int64_t x1 = (u + 1) * C / NUa;
+    d[1] = lo;
+    d[2] = kvh;
+    d[3] = t;
+    d[4] = (int)rem;  // < kTileCost + chunks of one tile
+    d[5] = seq;
+    d[6] = sv.q_len;
+    d[7] = sv.kv_total;
+    *(int64_t*)(d + 8) = sv.qs;
+    *(int64_t*)(d + 10) = sv.ctx;
+    *(int64_t*)(d + 12) = x0;
+    *(int64_t*)(d + 14) = x1;
+    d[0] = u;
   }
 }
 
@@ -2062,30 +2095,35 @@ __device__ void plan_prefill(const PAParams& p) {
 // kvh, t, c_lo, c_hi, partial, slot, rest, total)` computes chunks [c_lo, c_hi) of tile t.
 template <class TileFn>
 __device__ __forceinline__ void prefill_units(const PAParams& p, TileFn&& tile) {
+  // this workgroup's record (one 64-byte load) and the plan header, issued together and
+  // ahead of any store
+  static_assert(kPreRec == 16, "one i32x16 per record");
+  const i32x16 rec = *(const i32x16*)(p.ws_pre_unit + (int64_t)blockIdx.x * kPreRec);
+  const int64_t hdr_c = p.ws_plan_hdr[0], hdr_nua = p.ws_plan_hdr[1], hdr_npre = p.ws_plan_hdr[2];
   int32_t* job = p.ws_job + (int64_t)(kMaxDecodeWaves + blockIdx.x) * kJobInts;
   if (threadIdx.x == 0) job[0] = kJobNone;
-
-  const int64_t C = uni64(p.ws_plan_hdr[0]);
-  const int NUa = (int)uni64(p.ws_plan_hdr[1]);
-  const int n_pre = (int)uni64(p.ws_plan_hdr[2]);
-  if (C == 0 || NUa <= 0) return;
-  const int xcd = (int)(blockIdx.x % 8), j = (int)(blockIdx.x / 8);
-  const int q8 = NUa / 8, r8 = NUa % 8;
-  if (j >= q8 + (xcd < r8 ? 1 : 0)) return;  // idle workgroup (workgroup-uniform)
-  const int u = xcd * q8 + min(xcd, r8) + j;
-  int64_t x = u * C / NUa;
-  const int64_t x1 = (u + 1) * C / NUa;
-
-  const int32_t* ud = p.ws_pre_unit + (int64_t)u * 4;
-  int k = uni(ud[0]);
-  int kvh = uni(ud[1]);
-  int t = uni(ud[2]);
-  int seq = uni(p.ws_pre_list[k]);
-  SeqView sv = seq_view_uniform(p, seq);
+  const int u = uni(rec[0]);
+  if (u < 0) return;  // idle workgroup (workgroup-uniform)
+  const int64_t C = uni64(hdr_c);
+  const int NUa = (int)uni64(hdr_nua);
+  const int n_pre = (int)uni64(hdr_npre);
+  const auto pair = [&](int i) { return (int64_t)(((uint64_t)(uint32_t)rec[i + 1] << 32) | (uint32_t)rec[i]); };
+  int k = uni(rec[1]);
+  int kvh = uni(rec[2]);
+  int t = uni(rec[3]);
+  int64_t rem = uni(rec[4]);
+  int seq = uni(rec[5]);
+  SeqView sv;
+  sv.q_len = uni(rec[6]);
+  sv.kv_total = uni(rec[7]);
+  sv.qs = uni64(pair(8));
+  sv.ctx = uni64(pair(10));
+  int64_t x = uni64(pair(12));
+  const int64_t x1 = uni64(pair(14));
+  const int total = (int)(x1 - x);  // positions of this unit: < 2^31 (C / NUa + 1)
   int R = sv.q_len * p.G;
   int tiles = (R + p.PR - 1) / p.PR;
   int n_t = pre_tile_chunks(p, sv, R, t);
-  int64_t rem = uni(ud[3]);
   // a: this unit's first position within the tile. Positions a .. b - 1 of a tile are its
   // chunks max(0, a - kTileCost) .. max(0, b - kTileCost) - 1, the same map at both ends
   // of every unit, so the pieces partition the chunks; a range inside the virtual prefix is
@@ -2099,7 +2137,7 @@ __device__ __forceinline__ void prefill_units(const PAParams& p, TileFn&& tile) 
     if (c_hi > c_lo) {
       const bool whole = c_lo == 0 && c_hi == n_t;
       const int64_t slot = 2 * (int64_t)u + (first ? 0 : 1);
-      const int rest = (int)(x1 - (x + (b - a))), total = (int)(x1 - (u * C / NUa));
+      const int rest = (int)(x1 - (x + (b - a)));
       tile(sv, R, seq, kvh, t, c_lo, c_hi, !whole, slot, rest, total);
       if (threadIdx.x == 0 && c_lo == 0 && c_hi < n_t) {
         // the tile continues in units u + 1 .. u1, each holding it as its first piece

@@ -157,8 +157,8 @@ def test_workspace_follows_the_plan(lib):
     """Decode partial slots: one per (sequence, head group) plus one per possible decode work
     unit (8192 waves / 8 heads per unit when Hkv % 8 == 0), each holding RS = QS * G rows; merge-job records
     (16 int32) for 8192 decode units, plus 768 prefill units, their two 128-row partial
-    slots each and the prefill plan (sequence list, flat starts, unit starts) when the batch
-    has prefill-class queries."""
+    slots each and the prefill plan (sequence list, flat starts, one 64-byte record per prefill
+    workgroup) when the batch has prefill-class queries."""
     ws = lib.kvh_paged_attention_workspace_size
 
     def want(B, Hkv, G, QS, D, hgw=8, prefill=False):
@@ -167,7 +167,7 @@ def test_workspace_follows_the_plan(lib):
         up = lambda x: -(-x // 256) * 256  # noqa: E731
         jobs = 8192 + (768 if prefill else 0)
         prows = 2 * 768 * 128 if prefill else 0
-        plan = up(32) + up(B * 4) + up((B + 1) * 8) + up(768 * 16) if prefill else 0
+        plan = up(32) + up(B * 4) + up((B + 1) * 8) + up(768 * 64) if prefill else 0
         return up(rows * D * 4) + up(rows * 2 * 4) + up(jobs * 16 * 4) + up(prows * D * 4) + up(prows * 2 * 4) + plan
 
     assert ws(8, 8, 32, 8, 64, 32, 16, 1, 2) == want(8, 8, 4, 1, 64)  # C1
