@@ -1400,18 +1400,23 @@ __device__ __forceinline__ void pf_window(PfWindow& win, const PAParams& p, cons
   const int c = c0 + lane;
   const int r = p.BS / 16;  // 16-token halves per page (BS % 16 == 0)
   int id[2];
-  bool ok[2];
+  bool ok[2], in[2];
   int off[2];
+  int64_t raw[2];
+  // both loads are issued before either is used (one memory round trip). Every lane loads
+  // (column 0 when its page is outside the range: W >= 1), so the load is no divergent
+  // branch whose join could hold a spill store ahead of the exec restore.
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int hh = 2 * c + h;
     const int pg = hh / r;
     off[h] = (hh - pg * r) * 16;
-    // every lane loads (column 0 when its page is outside the range: W >= 1), so the load
-    // is no divergent branch whose join could hold a spill store ahead of the exec restore
-    const bool in = c < c_end && pg < page_end;
-    const int64_t raw = btrow[in ? pg : 0];
-    const int64_t b = in ? raw : -1;
+    in[h] = c < c_end && pg < page_end;
+    raw[h] = btrow[in[h] ? pg : 0];
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t b = in[h] ? raw[h] : -1;
     ok[h] = b >= 0 && b < p.num_blocks;
     id[h] = ok[h] ? (int)b : 0;
   }
@@ -1642,6 +1647,30 @@ struct PfPriority {
   }
 };
 
+// The query tile as the score MFMAs take it, and the exp2 argument's factor c: over bf16, Q
+// pre-scaled by scale log2(e) (c unused); otherwise the exp2 argument is fma(score, c, -m)
+// with c > 0: for a negative scale S c = (-Q) K^T |c| (a sign flip of Q is exact), for a
+// zero scale every score is 0 = (0 Q) K^T 1.
+template <class E, int D, int NT>
+__device__ __forceinline__ float pf_q_ready(WaveState<D, NT>& s, const PAParams& p) {
+  float c = fabsf(p.qk_scale);
+  if constexpr (kPrescaleQ<E>) {
+    pf_prescale_q<E, D, NT>(s, p.qk_scale);
+  } else if (p.qk_scale < 0.f) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int cc = 0; cc < D / 32; ++cc) s.q[t][cc] ^= 0x80008000u;
+  } else if (p.qk_scale == 0.f) {
+    c = 1.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int cc = 0; cc < D / 32; ++cc) s.q[t][cc] = u32x4{0u, 0u, 0u, 0u};
+  }
+  return c;
+}
+
 // One workgroup's pass over chunks [c_lo, c_hi) of tile t of (seq, kvh): the whole tile
 // (written out) or a piece of it (partial in slot `slot` of the prefill partial arrays).
 //
@@ -1670,35 +1699,19 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
   // keys below every valid row's causal limit (that of the wave's first row)
   const int lim_all = row0 < R ? (int)clamp64(sv.ctx + row0 / p.G + 1, 0, sv.kv_total) : 0;
 
-  WaveState<D, NT> s;
-  load_q<D, NT>(s, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
-  // Without pre-scaling, the exp2 argument is fma(score, c, -m) with c > 0: for a negative
-  // scale S c = (-Q) K^T |c| (a sign flip of Q is exact), for a zero scale every score is
-  // 0 = (0 Q) K^T 1.
-  float c = fabsf(p.qk_scale);
-  if constexpr (kPrescaleQ<E>) {
-    pf_prescale_q<E, D, NT>(s, p.qk_scale);
-  } else if (p.qk_scale < 0.f) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int cc = 0; cc < D / 32; ++cc) s.q[t][cc] ^= 0x80008000u;
-  } else if (p.qk_scale == 0.f) {
-    c = 1.f;
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int cc = 0; cc < D / 32; ++cc) s.q[t][cc] = u32x4{0u, 0u, 0u, 0u};
-  }
+  // the page window first: the first chunks' loads wait for it, the query tile is not
+  // needed before they are in flight
   const int64_t* btrow = p.bt + (int64_t)seq * p.bt_rs;
   const int page_end = (kv_lim + p.BS - 1) / p.BS;
   PfLoads<D> pl;
   pf_loads_init<D>(pl, p, w, kvh);
+  PfWindow win;
+  pf_window(win, p, btrow, c_lo, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
+  WaveState<D, NT> s;
+  load_q<D, NT>(s, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
   uint32_t ka[D / 32];
   pf_k_lanes<D>(ka, lds);
   const uint32_t vbase = lds_lane_addr(lds, 8);
-  PfWindow win;
-  pf_window(win, p, btrow, c_lo, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
 
   // every wave has finished reading the ring (previous tile) before it is refilled
   __builtin_amdgcn_sched_barrier(0);
@@ -1711,6 +1724,8 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
   int n_int = max(0, min(n_my, min(lim_all / kChunk, win.first_bad) - c_lo));
   pf_issue<D>(lds, 0, pl, win, c_lo);
   if (n > 1) pf_issue<D>(lds, L::kStageBytes, pl, win, c_lo + 1);
+  // Q and the page window were loaded together, Q is transformed while the first chunks load
+  const float c = pf_q_ready<E, D, NT>(s, p);
 
   PfPriority prio;
   prio.set(0, n, rest, total);
@@ -1820,32 +1835,19 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
   const int my_lim = row0 < R ? (int)clamp64(sv.ctx + my_last / p.G + 1, 0, sv.kv_total) : 0;
   const int lim_all = row0 < R ? (int)clamp64(sv.ctx + row0 / p.G + 1, 0, sv.kv_total) : 0;
 
-  WaveState<D, NT> s;
-  load_q<D, NT>(s, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
-  float c = fabsf(p.qk_scale);
-  if constexpr (kPrescaleQ<E>) {
-    pf_prescale_q<E, D, NT>(s, p.qk_scale);
-  } else if (p.qk_scale < 0.f) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int cc = 0; cc < D / 32; ++cc) s.q[t][cc] ^= 0x80008000u;
-  } else if (p.qk_scale == 0.f) {
-    c = 1.f;
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int cc = 0; cc < D / 32; ++cc) s.q[t][cc] = u32x4{0u, 0u, 0u, 0u};
-  }
+  // the page window first: the first chunks' loads wait for it, the query tile is not
+  // needed before they are in flight
   const int64_t* btrow = p.bt + (int64_t)seq * p.bt_rs;
   const int page_end = (kv_lim + p.BS - 1) / p.BS;
   PfLoads<D> pl;
   pf_loads_init<D, 1>(pl, p, w, kvh);
+  PfWindow win;
+  pf_window(win, p, btrow, c_lo, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
+  WaveState<D, NT> s;
+  load_q<D, NT>(s, p, sv.qs, R, row0, kvh, sv.ctx, sv.kv_total);
   uint32_t ka[D / 32];
   pf_k_lanes<D>(ka, lds);
   const uint32_t vbase = lds_lane_addr(lds, 8);
-  PfWindow win;
-  pf_window(win, p, btrow, c_lo, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
 
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();  // every wave has finished reading the stages (previous tile)
@@ -1870,6 +1872,7 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
   };
   issue(raw[0], c_lo);
   if (n > 1) issue(raw[1], c_lo + 1);
+  const float c = pf_q_ready<E, D, NT>(s, p);
 
   PfPriority prio;  // wave priority as in prefill_tile
   prio.set(0, n, rest, total);
