@@ -10,7 +10,8 @@ namespace kvh {
 // Upper bound on the waves one decode launch uses (256 CUs x 8 waves per SIMD x 4 SIMDs
 // would be 8192); the workspace is sized for it, so its size never depends on the device.
 constexpr int32_t kMaxDecodeWaves = 8192;
-// Upper bound on the workgroups (work units) of one prefill launch: 256 CUs x 3 resident.
+// Workgroup slots of the prefill workspace: 256 CUs x 3 tiles of kPrefillRows rows; a launch
+// of PR-row tiles takes at most kMaxPrefillUnits x kPrefillRows / PR units (512 at PR = 192).
 constexpr int32_t kMaxPrefillUnits = 768;
 // Query rows ((token, head) pairs of one kv head) of one prefill workgroup's tile; the
 // prefill workspace holds 2 slots x kMaxPrefillUnits x kPrefillRows partial rows, and a

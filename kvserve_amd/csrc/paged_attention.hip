@@ -42,7 +42,12 @@ namespace kvh {
 
 constexpr int kChunk = 32;  // tokens per wave iteration
 constexpr int kWavesPerWG = 4;
-constexpr int kPrefillNQT = 2;  // 16-row tiles per prefill wave
+// 16-row tiles per prefill wave: 3 over 16-bit caches (48 rows, 254 VGPRs, 2 workgroups per
+// CU), 2 over E4M3 caches (whose conversion registers leave no room for a third)
+template <bool KV8>
+constexpr int prefill_nt() {
+  return KV8 ? 2 : 3;
+}
 
 // ---------------------------------------------------------------------------------------
 // Block ids of 64 consecutive pages, one per lane; -1 marks a page that must not be read
@@ -1116,7 +1121,7 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
 }
 
 // Log-sum-exp merge of split segments. A job covers `rows` partial rows per piece (HGW
-// heads x RS rows for decode, kPrefillRows rows of one head for prefill); row x of piece i
+// heads x RS rows for decode, PAParams::PR rows of one head for prefill); row x of piece i
 // sits at (slot(i) * rows + x) in the partial arrays. Each workgroup merges MR = 1024 / D
 // rows of one job: workgroups 0 .. NU * CD - 1 take decode unit b / CD, rows MR (b % CD) ..;
 // the next NUP * (128 / MR) take prefill record b' / (128 / MR), rows MR (b' % (128 / MR)) ...
@@ -1294,8 +1299,9 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Prefill class (q_len > QS): a workgroup of 4 waves computes kPrefillRows = 128 query rows
-// of one (sequence, kv head), wave w holding rows 32 w .. 32 w + 31 of the tile.
+// Prefill class (q_len > QS): a workgroup of 4 waves computes 64 NT query rows of one
+// (sequence, kv head) (PAParams::PR: 192 over 16-bit caches, 128 over E4M3 caches), wave w
+// holding rows 16 NT w .. 16 NT (w + 1) - 1 of the tile.
 //
 // The 4 waves share every 32-key K/V chunk through a 3-stage LDS ring filled by direct
 // global->LDS loads (no VGPR staging): chunk c + 2 is in flight while chunk c is computed.
@@ -1685,12 +1691,13 @@ template <class E, int D>
 __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const SeqView& sv, int R, int seq,
                                              int kvh, int t, int c_lo, int c_hi, int w, bool partial,
                                              int64_t slot, int rest, int total) {
-  constexpr int NT = kPrefillNQT;
+  constexpr int NT = prefill_nt<false>();
+  constexpr int PRW = kWavesPerWG * 16 * NT;  // rows of a tile
   using L = PrefillLds<D>;
   c_lo = uni(c_lo);
   c_hi = uni(c_hi);
-  const int wg_row0 = t * kPrefillRows;
-  const int wg_last = min(wg_row0 + kPrefillRows - 1, R - 1);
+  const int wg_row0 = t * PRW;
+  const int wg_last = min(wg_row0 + PRW - 1, R - 1);
   const int kv_lim = (int)clamp64(sv.ctx + wg_last / p.G + 1, 0, sv.kv_total);
   const int row0 = wg_row0 + w * 16 * NT;
   const int my_last = min(row0 + 16 * NT - 1, R - 1);
@@ -1806,7 +1813,7 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
     stg = stg == 2 ? 0 : stg + 1;
   }
   if constexpr (kPrescaleQ<E>) pf_prescale_finish<D, NT>(s);
-  pf_write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, slot * kPrefillRows - wg_row0);
+  pf_write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, slot * PRW - wg_row0);
 }
 
 // prefill_tile over an E4M3 cache. Direct global->LDS loads cannot convert, so each lane
@@ -1820,15 +1827,16 @@ template <class E, int D>
 __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, const SeqView& sv, int R, int seq,
                                                  int kvh, int t, int c_lo, int c_hi, int w, bool partial,
                                                  int64_t slot, int rest, int total) {
-  constexpr int NT = kPrefillNQT;
+  constexpr int NT = prefill_nt<true>();
+  constexpr int PRW = kWavesPerWG * 16 * NT;  // rows of a tile
   using L = PrefillLds<D>;
   constexpr int KLW = L::kLoadsPerWave;
   typedef __attribute__((address_space(3))) u32x4* lds_u32x4_ptr;
   c_lo = uni(c_lo);
   c_hi = uni(c_hi);
   const int lane = threadIdx.x & 63;
-  const int wg_row0 = t * kPrefillRows;
-  const int wg_last = min(wg_row0 + kPrefillRows - 1, R - 1);
+  const int wg_row0 = t * PRW;
+  const int wg_last = min(wg_row0 + PRW - 1, R - 1);
   const int kv_lim = (int)clamp64(sv.ctx + wg_last / p.G + 1, 0, sv.kv_total);
   const int row0 = wg_row0 + w * 16 * NT;
   const int my_last = min(row0 + 16 * NT - 1, R - 1);
@@ -1955,7 +1963,7 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
     if (i < n_my) compute(i, (i & 1) * L::kStageBytes, S0{}, std::true_type{});
   }
   if constexpr (kPrescaleQ<E>) pf_prescale_finish<D, NT>(s);
-  pf_write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, slot * kPrefillRows - wg_row0);
+  pf_write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, slot * PRW - wg_row0);
 }
 
 // Chunks of tile t (rows 128 t .. of R): those its last row can see, at least one so that
@@ -2168,9 +2176,9 @@ __device__ __forceinline__ void prefill_units(const PAParams& p, TileFn&& tile) 
   }
 }
 
-// 4-wave workgroups of kPrefillRows = 128 rows (PAParams::PR).
+// 4-wave workgroups of 64 NT rows (PAParams::PR), 2 per CU.
 template <class E, int D, bool KV8>
-__global__ __launch_bounds__(256, KV8 ? 2 : 3) void pa_prefill_kernel(PAParams p) {
+__global__ __launch_bounds__(256, 2) void pa_prefill_kernel(PAParams p) {
   using L = PrefillLds<D>;
   __shared__ __attribute__((aligned(1024))) char lds[(KV8 ? 2 : L::kStages) * L::kStageBytes];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -2253,7 +2261,7 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipSt
   if (plan.launch_prefill) {
     // the unit count is fixed before the decode launch: both kernels write merge jobs. Units x
     // 2 partial slots x tile rows stay within the workspace's kMaxPrefillUnits x 2 x kPrefillRows.
-    p.PR = kPrefillRows;
+    p.PR = kWavesPerWG * 16 * prefill_nt<KV8>();
     int units = resident_blocks((const void*)&pa_prefill_kernel<E, D, KV8>);
     const int cap = kMaxPrefillUnits * kPrefillRows / p.PR;
     if (units > cap) units = cap;
