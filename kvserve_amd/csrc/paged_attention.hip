@@ -1742,7 +1742,9 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
     const int ci2 = c_lo + i + 2;
     if (i + 2 < n && ci2 - win.c0 >= 64) {  // the window moves on (every 62 chunks)
       pf_window(win, p, btrow, c_lo + i, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
-      n_int = min(n_int, win.first_bad - c_lo);
+      // the unmasked run reaches as far as the new window allows (the old window's end
+      // capped it; a missing page before this point has already ended the run)
+      n_int = max(0, min(n_my, min(lim_all / kChunk, win.first_bad) - c_lo));
     }
     __builtin_amdgcn_sched_barrier(0);
     if (i + 1 < n)
@@ -1891,7 +1893,9 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
     const int ci2 = c_lo + i + 2;
     if (i + 2 < n && ci2 - win.c0 >= 64) {
       pf_window(win, p, btrow, c_lo + i, c_hi, page_end, pl.h, pl.sb2, pl.ss2);
-      n_int = min(n_int, win.first_bad - c_lo);
+      // the unmasked run reaches as far as the new window allows (the old window's end
+      // capped it; a missing page before this point has already ended the run)
+      n_int = max(0, min(n_my, min(lim_all / kChunk, win.first_bad) - c_lo));
     }
     __builtin_amdgcn_sched_barrier(0);
     if (i + 1 < n)
