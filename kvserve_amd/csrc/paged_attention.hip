@@ -1641,8 +1641,8 @@ __device__ __forceinline__ void wait_vm() {
 // 3 / kPrioSteps of the unit's work (eighths: the workgroups on a CU stay closer at the end
 // than with quarters, C3 2% faster; sixteenths gain nothing more). It only falls as i grows,
 // so it is set at a tile's first chunk and again at the chunks where it drops: lvl(i) >= k
-// exactly for i <= rest + n - ceil(k (total + 1) / kPrioSteps). (Checked against the
-// per-chunk formula for every total < 120, n < 40 and rest.)
+// exactly for i <= rest + n - ceil(k (total + 1) / kPrioSteps). (A host test evaluates both
+// expressions from this source against the per-chunk formula.)
 constexpr int kPrioSteps = 8;
 struct PfPriority {
   int next_drop;  // first chunk whose level is below the current one

@@ -490,3 +490,30 @@ def test_built_kernels_have_no_partial_exec_spills():
     if not asms:
         pytest.skip("no device assembly: run python -m kvserve_amd.build")
     assert [hit for a in asms for hit in isa_check.check(a.read_text())] == []
+
+
+def test_prefill_priority_change_points_match_the_per_chunk_level():
+    """The prefill kernel sets a wave's priority level only at a tile's first chunk and at
+    the chunks its `next_drop` names; the level it holds must equal the per-chunk level
+    min(3, K left / (total + 1)) at every chunk. Both expressions are taken from the source."""
+    src = (Path(__file__).resolve().parent.parent / "kvserve_amd/csrc/paged_attention.hip").read_text()
+    steps = int(re.search(r"constexpr int kPrioSteps = (\d+);", src).group(1))
+    lvl_src = re.search(r"const int lvl = (min\(3, .*?\));", src).group(1)
+    drop_src = re.search(r"next_drop = lvl > 0 \? (.*?) : INT32_MAX;", src).group(1)
+
+    def py(expr):  # the expressions are non-negative integer arithmetic: C / is floor division
+        return expr.replace("kPrioSteps", str(steps)).replace("/", "//")
+
+    lvl_of = eval("lambda i, n, rest, total: " + py(lvl_src))  # noqa: S307 (source text of this repo)
+    drop_of = eval("lambda lvl, n, rest, total: " + py(drop_src))  # noqa: S307
+    big = 1 << 31
+    for total in range(1, 90):
+        for n in range(1, min(total, 30) + 1):
+            for rest in range(0, total - n + 1):
+                lvl = lvl_of(0, n, rest, total)
+                nxt = drop_of(lvl, n, rest, total) if lvl > 0 else big
+                for i in range(n):
+                    if i >= nxt:
+                        lvl = lvl_of(i, n, rest, total)
+                        nxt = drop_of(lvl, n, rest, total) if lvl > 0 else big
+                    assert lvl == lvl_of(i, n, rest, total), (total, n, rest, i)
