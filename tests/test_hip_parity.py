@@ -367,3 +367,35 @@ def test_strided_cache_layouts(hip_device, layout, fp8):
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
     if not fp8:  # E4M3 attention against the oracle: tests/test_hip_fp8.py
         assert pc.max_err_vs_oracle(b, ref, list(range(len(w.query_lens)))) <= pc.TOL_16BIT
+
+
+def test_prefill_page_outside_the_pool_after_the_first_window(hip_device):
+    """A block-table entry outside the pool is a missing page: its 16 keys take no part in
+    the softmax (the prefill kernel reads block 0 for it and masks the keys). Placed past the
+    first 64 chunks of long stream-K pieces (8 x 2048 queries over 2048 cached tokens), it
+    also pins that a page-window refresh extends the unmasked run only up to such a page.
+    Expected rows are computed here in fp64 from the cache without those keys."""
+    H, Hkv, D, BS = 32, 8, 128, 16
+    w = workloads.custom("missing_page", [2048] * 8, [2048] * 8, H, Hkv, D, BS, seed=11)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=11)
+    seq, page = 3, 200  # tokens 3200 .. 3215 of sequence 3
+    b.meta.block_tables[seq, page] = w.num_blocks + 7
+    out = pc.attend(b)
+    assert "prefill" in last_launch_kernels()
+    G, ctx, q0 = H // Hkv, w.seq_lens[seq] - w.query_lens[seq], sum(w.query_lens[:seq])
+    table = torch.tensor(w.tables[seq], dtype=torch.long, device=hip_device)
+    kc = b.k_cache.index_select(0, table).to(torch.float64).cpu().reshape(-1, Hkv, D).numpy()
+    vc = b.v_cache.index_select(0, table).to(torch.float64).cpu().reshape(-1, Hkv, D).numpy()
+    keep = np.ones(kc.shape[0], dtype=bool)
+    keep[page * BS : (page + 1) * BS] = False
+    err = 0.0
+    for i in (100, 1151, 1152, 1500, 2047):  # rows before, at and past the missing page
+        lim = ctx + i + 1
+        sel = np.nonzero(keep[:lim])[0]
+        q = b.q[q0 + i].to(torch.float64).cpu().numpy()
+        for h in (0, 5, 13, 31):
+            s = kc[sel, h // G] @ q[h] * w.scale
+            p = np.exp(s - s.max())
+            ref = p @ vc[sel, h // G] / p.sum()
+            err = max(err, float(np.abs(ref - out[q0 + i, h].float().cpu().numpy()).max()))
+    assert err <= pc.TOL_16BIT, err
