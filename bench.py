@@ -3,6 +3,7 @@
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-secondary]
     python bench.py --only N [--fp8]      # one BASELINE config (E4M3 KV caches with --fp8)
+    python bench.py --sweep               # the reference's decode-kernel grid (bench/bench_kernel.py)
 
 Headline workload: BASELINE config 2 (Llama-3.1-8B decode layer: 64 sequences, 32 q / 8 kv
 heads, head_dim 128, block 16, contexts U[1024, 8192], bf16), the config the metric is
@@ -214,6 +215,75 @@ def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0, f
     del b
     torch.cuda.empty_cache()
     return res
+
+
+# The reference's kernel sweep (bench/bench_kernel.py:58-82): 32 q / 8 kv heads, head_dim 64,
+# block 16, bf16, one query per sequence over ctx - 1 cached tokens, batch x ctx with
+# batch * ctx <= 64 * 8192; bytes = 2 B ctx Hkv D 2 (:81). Its published RTX 4090 figures
+# (results/rtx4090/kernel_decode_attention.jsonl:1-14, 1008 GB/s peak) sit beside each point.
+SWEEP_RTX4090_GBS = {
+    (1, 512): 34.1, (1, 2048): 39.0, (1, 8192): 40.7, (8, 512): 234.1, (8, 2048): 292.6, (8, 8192): 308.5,
+    (32, 512): 555.4, (32, 2048): 645.7, (32, 8192): 827.0, (64, 512): 619.0, (64, 2048): 773.7,
+    (64, 8192): 900.1, (128, 512): 636.3, (128, 2048): 847.0,
+}  # fmt: skip
+
+
+def measure_sweep(iters: int = 50, warmup: int = 5) -> list[dict]:
+    """The reference's decode-kernel grid on this GPU: the forward call (every kernel it launches)
+    timed with events around it, each call after a 1 GiB read that evicts the caches (the
+    reference flushes 256 MB for a 72 MB L2), median of `iters`; GB/s on the reference's byte
+    formula and as a fraction of 8 TB/s. One JSON line per point."""
+    import torch
+
+    from kvserve_amd import HipAttention, _lib, last_launch_kernels, workloads
+
+    H, Hkv, D, BS = 32, 8, 64, 16
+    flush = torch.zeros(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda:0")
+    lib = _lib.load()
+    ev = HipEvents(5)
+    rows = []
+    for batch in (1, 8, 32, 64, 128):
+        for ctx in (512, 2048, 8192):
+            if batch * ctx > 64 * 8192:
+                continue
+            w = workloads.custom(f"sweep_b{batch}_c{ctx}", [1] * batch, [ctx - 1] * batch, H, Hkv, D, BS, seed=0)
+            b = workloads.materialize(w, torch.bfloat16, "cuda:0", seed=0)
+            HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping)
+            out = torch.empty_like(b.q)
+
+            def fwd():
+                return HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale, out=out)
+
+            for _ in range(warmup):
+                fwd()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            times, kern = [], []
+            for _ in range(iters):
+                flush.amax()
+                lib.kvh_profile_arm(ev.array, 5)
+                start.record()
+                fwd()
+                end.record()
+                end.synchronize()
+                times.append(start.elapsed_time(end))
+                kinds = last_launch_kernels()
+                kern.append(ev.elapsed_ms(0, len(kinds[:4])))
+            ms = statistics.median(times)
+            kms = statistics.median(kern)
+            kv_bytes = 2 * batch * ctx * Hkv * D * 2
+            gbs = kv_bytes / (ms * 1e-3) / 1e9
+            ref = SWEEP_RTX4090_GBS.get((batch, ctx))
+            row = {
+                "batch": batch, "ctx": ctx, "ms": ms, "gbs": gbs, "frac_hbm": gbs / HBM_PEAK_GBS,
+                "kernels": kinds, "kernels_ms": kms, "kernels_gbs": kv_bytes / (kms * 1e-3) / 1e9,
+                "rtx4090_gbs": ref, "rtx4090_frac": None if ref is None else ref / 1008.0,
+            }  # fmt: skip
+            print(json.dumps(row), flush=True)
+            rows.append(row)
+            del b, out
+            torch.cuda.empty_cache()
+    ev.close()
+    return rows
 
 
 def cpu_baseline(idx: int, budget_s: float, seed: int = 0) -> dict:
@@ -466,6 +536,8 @@ def main() -> int:
     p.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
     p.add_argument("--no-engine", action="store_true", help="skip the 1B/8B engine decode tokens/s")
     p.add_argument("--engine-only", action="store_true", help="run just the engine decode tokens/s")
+    p.add_argument("--sweep", action="store_true",
+                   help="the reference's decode-kernel grid (32/8 heads, D 64, batch x ctx) beside its RTX 4090 GB/s")
     p.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = p.parse_args()
     if args.pmc_child:
@@ -491,6 +563,9 @@ def main() -> int:
 
     if args.only:
         print(json.dumps(measure(args.only, args.steps, args.warmup, args.prof_iters, fp8=args.fp8)), flush=True)
+        return 0
+    if args.sweep:
+        measure_sweep()
         return 0
     engine_batches = {"llama_3_2_1b": [1, 8, 32, 64, 128], "llama_3_1_8b": [1, 8, 32, 64]}
     if args.engine_only:

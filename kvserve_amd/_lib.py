@@ -22,7 +22,7 @@ ABI_VERSION = 1
 
 KVH_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
-KERNEL_KINDS = {1: "decode", 2: "prefill", 3: "reduce", 4: "f32", 5: "share"}
+KERNEL_KINDS = {1: "decode", 2: "prefill", 3: "reduce", 4: "f32", 5: "share", 6: "valu16"}
 
 _i32, _i64, _f32, _vp, _sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
 _i64p = ctypes.POINTER(ctypes.c_int64)

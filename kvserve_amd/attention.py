@@ -5,7 +5,7 @@ Mirrors src/kvserve/attention.py of the reference:
   * `HipAttention` is a class used as a namespace of static methods with the exact
     `write_kv` / `forward` signatures of the reference's backends (attention.py:39-82,
     :88-102), so `Attention.attend` (model.py:96-108) calls it unchanged;
-  * `get_backend(name, device, block_size, fallback)` keeps the reference's selector contract
+  * `get_backend(name, device, block_size, fallback, head_dim)` keeps the reference's selector contract
     (attention.py:113-124) for the names this package serves ("hip", and "auto", which
     falls back instead of raising).
 
@@ -376,29 +376,47 @@ def hip_available() -> bool:
     return True
 
 
-def hip_eligible(device: str, block_size: int) -> bool:
-    """True when the HIP backend can serve this engine: a ROCm device, libkvhip loaded and a
-    block size the 16-token MFMA tiles divide."""
+# Head sizes the MFMA kernels take; the vector-ALU kernel serves any other head size of whole
+# 16-byte rows up to 256 (correct, at a fraction of the bandwidth).
+MFMA_HEAD_DIMS = (64, 128)
+
+
+def head_dim_supported(head_dim: int) -> bool:
+    """A head size HipAttention computes at all (bf16 / fp16: a multiple of 8 up to 256)."""
+    return 0 < head_dim <= 256 and head_dim % 8 == 0
+
+
+def hip_eligible(device: str, block_size: int, head_dim: int | None = None) -> bool:
+    """True when the HIP backend serves this engine at speed: a ROCm device, libkvhip loaded, a
+    block size the 16-token MFMA tiles divide and (when the caller passes it) a head size the
+    MFMA kernels take (64 or 128)."""
+    if head_dim is not None and head_dim not in MFMA_HEAD_DIMS:
+        return False
     return str(device).startswith("cuda") and block_size >= 16 and block_size % 16 == 0 and hip_available()
 
 
-def get_backend(name: str, device: str, block_size: int, fallback=None):
+def get_backend(name: str, device: str, block_size: int, fallback=None, head_dim: int | None = None):
     """Selector with the reference's contract (src/kvserve/attention.py:113-124).
 
     "auto" never raises, as in the reference: it resolves to HipAttention when the backend can
-    run here (`hip_eligible`), otherwise to `fallback` -- the backend the caller's own "auto"
-    would pick (kvserve passes its torch / triton choice; None when not given). "hip" raises
-    RuntimeError when the backend cannot run and ValueError for a block size the kernels do
-    not tile, like the reference's "triton". The reference's "torch" and "triton" names stay
-    with its own classes: this package ships no CPU path.
+    run here at speed (`hip_eligible`; pass `head_dim` so that a model whose heads the MFMA
+    kernels do not take -- anything but 64 and 128 -- keeps the caller's choice), otherwise to
+    `fallback` -- the backend the caller's own "auto" would pick (kvserve passes its torch /
+    triton choice; None when not given). "hip" raises RuntimeError when the backend cannot run
+    and ValueError for a block size the kernels do not tile or a head size they cannot compute
+    (not a multiple of 8, or above 256), like the reference's "triton"; other head sizes run on
+    the vector-ALU kernel. The reference's "torch" and "triton" names stay with its own classes:
+    this package ships no CPU path.
     """
     if name == "auto":
-        return HipAttention if hip_eligible(device, block_size) else fallback
+        return HipAttention if hip_eligible(device, block_size, head_dim) else fallback
     if name == "hip":
         if not hip_available():
             raise RuntimeError("hip backend needs a ROCm GPU and a built kvserve_amd/lib/libkvhip.so")
         if block_size < 16 or block_size % 16 != 0:
             raise ValueError("hip backend needs block_size a multiple of 16 (16-token MFMA tiles)")
+        if head_dim is not None and not head_dim_supported(head_dim):
+            raise ValueError(f"hip backend computes head sizes that are multiples of 8 up to 256, not {head_dim}")
         return HipAttention
     if name in ("torch", "triton"):
         raise ValueError(f"backend {name!r} belongs to kvserve.attention; kvserve_amd serves 'hip' and 'auto'")

@@ -4,9 +4,9 @@
 
 Objects go to kvserve_amd/_build/, the library to kvserve_amd/lib/. Both are git-ignored
 build products; the library travels with the source tree so a GPU host needs no compiler.
-Every source's device code is also compiled to assembly (same flags) and checked for spill
-stores the compiler placed where part of the wave is disabled (kvserve_amd/isa_check.py); a
-library with one is not linked.
+Each object is compiled with -save-temps, so the gfx950 assembly that the assembler turned into
+that very object is kept next to it; it is checked for spill stores the compiler placed where
+part of the wave is disabled (kvserve_amd/isa_check.py), and a library with one is not linked.
 """
 
 from __future__ import annotations
@@ -119,31 +119,29 @@ def build(
     cc = hipcc()
     flags = HIP_FLAGS + list(extra_flags or [])
 
-    def compile_one(src: str) -> Path:
+    def compile_one(src: str) -> tuple[Path, Path]:
+        # -save-temps=obj keeps the intermediate files next to the object; among them the
+        # device assembly that was assembled into this object (no second compilation)
         obj = objdir / (Path(src).stem + ".o")
-        cmd = [cc, *flags, *SOURCE_FLAGS.get(src, []), f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)]
+        asm = objdir / (Path(src).stem + "-hip-amdgcn-amd-amdhsa-gfx950.s")
+        asm.unlink(missing_ok=True)
+        cmd = [cc, *flags, *SOURCE_FLAGS.get(src, []), f"-I{INCLUDE}", "-save-temps=obj", "-c", str(CSRC / src),
+               "-o", str(obj)]  # fmt: skip
         if verbose:
             print(" ".join(cmd))
         _run(cmd)
-        return obj
+        if not asm.exists():
+            raise RuntimeError(f"the device assembly of {src} was not kept ({asm.name})")
+        return obj, asm
 
-    def assemble_one(src: str) -> Path:
-        # the same device compilation as compile_one, stopped at the assembly
-        asm = objdir / (Path(src).stem + ".gfx950.s")
-        cmd = [cc, *flags, *SOURCE_FLAGS.get(src, []), f"-I{INCLUDE}", "--cuda-device-only", "-S", str(CSRC / src),
-               "-o", str(asm)]  # fmt: skip
-        _run(cmd)
-        return asm
-
-    jobs = min(2 * len(SOURCES), int(os.environ.get("MAX_JOBS", "8")), 16)
+    jobs = min(len(SOURCES), int(os.environ.get("MAX_JOBS", "8")), 16)
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        # the two slowest compilations (paged_attention's object and assembly) start first
+        # the slowest compilation (paged_attention) starts first
         order = sorted(SOURCES, key=lambda s: s != "paged_attention.hip")
-        asm_futs = {s: ex.submit(assemble_one, s) for s in order}
-        obj_futs = {s: ex.submit(compile_one, s) for s in order}
-        objs = [obj_futs[s].result() for s in SOURCES]
-        asms = [asm_futs[s].result() for s in SOURCES]
-    bad = [f"{asm.name}: {hit}" for asm in asms for hit in isa_check.check(asm.read_text())]
+        futs = {s: ex.submit(compile_one, s) for s in order}
+        built = [futs[s].result() for s in SOURCES]
+    objs = [obj for obj, _ in built]
+    bad = [f"{asm.name}: {hit}" for _, asm in built for hit in isa_check.check(asm.read_text())]
     if bad:
         raise RuntimeError(
             "the compiler placed spill stores where some lanes are disabled (their reloads would hand those "

@@ -57,7 +57,8 @@ Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t 
   pl.RS = pl.QS * G;
   pl.HGW = Hkv % 8 == 0 ? 8 : (Hkv % 4 == 0 ? 4 : (Hkv % 2 == 0 ? 2 : 1));
   pl.slots = (int64_t)B * Hkv / pl.HGW + kMaxDecodeWaves / pl.HGW;
-  if (dtype == KVH_DTYPE_F32) {
+  pl.short_decode = !pl.launch_prefill && pl.NT == 1 && (int64_t)W * BS <= kShortTokens;
+  if (dtype == KVH_DTYPE_F32 || !mfma_shape(D, BS, G) || pl.short_decode) {
     pl.ws_acc_bytes = pl.ws_ml_bytes = pl.ws_job_bytes = pl.ws_pacc_bytes = pl.ws_pml_bytes = pl.ws_plan_bytes =
         pl.ws_bytes = 0;
   } else {
@@ -125,10 +126,11 @@ int kvh_reshape_and_cache(const void* k, int64_t k_tok_stride, int64_t k_head_st
   if (dtype < KVH_DTYPE_F32 || dtype > KVH_DTYPE_BF16) return KVH_E_DTYPE;
   if (num_tokens < 0 || num_blocks < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0)
     return KVH_E_SHAPE;
-  if (num_tokens > 0x7fffffffLL) return KVH_E_SHAPE;
+  const int eb = elem_bytes(dtype);
+  // a token's K and V rows are indexed with 32-bit integers (element copies at worst)
+  if (num_tokens > 0x7fffffffLL || (int64_t)num_kv_heads * head_dim * eb > (1 << 26)) return KVH_E_SHAPE;
   if (num_tokens == 0) return KVH_OK;
   if (!k || !v || !k_cache || !v_cache || !k_cache_strides || !v_cache_strides || !slot_mapping) return KVH_E_NULL;
-  const int eb = elem_bytes(dtype);
   const int64_t strides[] = {k_tok_stride, k_head_stride, v_tok_stride, v_head_stride,
                              k_cache_strides[0], k_cache_strides[1], k_cache_strides[2],
                              v_cache_strides[0], v_cache_strides[1], v_cache_strides[2]};
@@ -155,7 +157,7 @@ int kvh_reshape_and_cache_fp8(const void* k, int64_t k_tok_stride, int64_t k_hea
   if (num_tokens < 0 || num_blocks < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0)
     return KVH_E_SHAPE;
   if (!(k_scale > 0.f && k_scale < INFINITY && v_scale > 0.f && v_scale < INFINITY)) return KVH_E_SHAPE;
-  if (num_tokens > 0x7fffffffLL || (int64_t)num_kv_heads * head_dim / 4 > 0x7fffffffLL) return KVH_E_SHAPE;
+  if (num_tokens > 0x7fffffffLL || (int64_t)num_kv_heads * head_dim > (1 << 26)) return KVH_E_SHAPE;
   if (head_dim % 8 != 0) return KVH_E_UNSUPPORTED;
   if (num_tokens == 0) return KVH_OK;
   if (!k || !v || !k_cache || !v_cache || !k_cache_strides || !v_cache_strides || !slot_mapping) return KVH_E_NULL;
@@ -298,14 +300,8 @@ static int check_attention_shape(int64_t num_tokens, int32_t num_seqs, int32_t n
   // query rows (token, head of a group) are indexed with 32-bit integers
   if (num_tokens * (num_heads / num_kv_heads) > 0x7fffffffLL) return KVH_E_UNSUPPORTED;
   if ((int64_t)max_blocks_per_seq * block_size >= 0x7fffffffLL) return KVH_E_UNSUPPORTED;
-  if (dtype == KVH_DTYPE_F32) {
-    if (head_dim % 4 != 0 || head_dim > 256) return KVH_E_UNSUPPORTED;
-  } else {
-    if (head_dim != 64 && head_dim != 128) return KVH_E_UNSUPPORTED;
-    if (block_size % 16 != 0) return KVH_E_UNSUPPORTED;
-    // the split-K kernel keeps at most 4 tiles of 16 query rows in registers
-    if (num_heads / num_kv_heads > 64) return KVH_E_UNSUPPORTED;
-  }
+  // rows of whole 16-byte vectors, at most 256 elements (the vector-ALU kernel's query row)
+  if (head_dim % (dtype == KVH_DTYPE_F32 ? 4 : 8) != 0 || head_dim > 256) return KVH_E_UNSUPPORTED;
   return KVH_OK;
 }
 
@@ -350,7 +346,9 @@ static int paged_attention_impl(const void* q, int64_t q_tok_stride, int64_t q_h
   // num_blocks >= 1: the kernels read block 0 in place of an absent tile (and mask it out)
   if (num_blocks < 1 || bt_row_stride < max_blocks_per_seq) return KVH_E_SHAPE;
   if (kv8) {
-    if (dtype == KVH_DTYPE_F32) return KVH_E_UNSUPPORTED;  // E4M3 caches feed the 16-bit MFMA path
+    // E4M3 caches feed the 16-bit MFMA path only
+    if (dtype == KVH_DTYPE_F32 || !mfma_shape(head_dim, block_size, num_heads / num_kv_heads))
+      return KVH_E_UNSUPPORTED;
     if (!(k_scale > 0.f && k_scale < INFINITY && v_scale > 0.f && v_scale < INFINITY)) return KVH_E_SHAPE;
   }
   const int64_t strides[] = {q_tok_stride, q_head_stride, o_tok_stride, o_head_stride,
@@ -449,8 +447,8 @@ static int paged_attention_impl(const void* q, int64_t q_tok_stride, int64_t q_h
     log.num_events = n_armed;
     if (armed[0]) (void)hipEventRecord((hipEvent_t)armed[0], s);
   }
-  if (dtype == KVH_DTYPE_F32)
-    st = launch_paged_attention_f32(p, head_dim, max_query_len < 1 ? 1 : max_query_len, s, log);
+  if (dtype == KVH_DTYPE_F32 || !mfma_shape(head_dim, block_size, plan.G))
+    st = launch_paged_attention_valu(p, head_dim, dtype, max_query_len < 1 ? 1 : max_query_len, s, log);
   else
     st = launch_paged_attention_mfma(p, plan, head_dim, dtype, kv8, max_query_len < 1 ? 1 : max_query_len, s, log);
   g_prof.last_count = log.launched;

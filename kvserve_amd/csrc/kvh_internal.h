@@ -22,6 +22,11 @@ constexpr int32_t kPrefillRows = 128;
 // when the cascade members (decode-class sequences with at least kCascadeMinChunks chunks of
 // context) share at least kCascadeMinChunks chunks of table prefix.
 constexpr int32_t kCascadeMinTokens = 8192;
+// Short decode: a decode-only batch of single-tile rows whose block tables hold at most
+// kShortTokens keys takes one workgroup per (sequence, kv head); its 4 waves split the chunks
+// and combine their partials in LDS, so nothing goes through the workspace and no merge
+// launch follows.
+constexpr int32_t kShortTokens = 1024;
 constexpr int32_t kCascadeMinChunks = 8;
 constexpr int32_t kShareHdr = 8;  // int64: shared tokens, prefix groups, row of the shared table, sequences
 // Merge job record: int32 fields, one record per work unit (decode units first).
@@ -87,6 +92,7 @@ struct Plan {
   int32_t HGW;              // kv heads per decode work unit
   bool launch_prefill;      // max_query_len > QS
   bool cascade;             // the share kernel runs and the decode kernel may take the cascade path
+  bool short_decode;        // one workgroup per (sequence, kv head), no workspace, no merge
   int32_t SG;               // cascade: sequences per prefix group
   int64_t xslots;           // cascade: prefix partial slots
   int64_t slots;            // partial slots: B * Hkv / HGW + kMaxDecodeWaves / HGW
@@ -107,7 +113,14 @@ struct LaunchLog {
 
 int launch_paged_attention_mfma(PAParams& p, const Plan& plan, int32_t D, int32_t dtype, bool kv8, int32_t max_q,
                                 hipStream_t s, LaunchLog& log);
-int launch_paged_attention_f32(const PAParams& p, int32_t D, int32_t max_q, hipStream_t s, LaunchLog& log);
+// Whether a 16-bit launch takes the MFMA kernels: head sizes 64 and 128, pages a whole number
+// of 16-token tiles, GQA groups of at most 64 rows per token (four 16-row tiles). Every other
+// 16-bit shape, and fp32, takes the vector-ALU kernel (no workspace).
+inline bool mfma_shape(int32_t D, int32_t BS, int32_t G) {
+  return (D == 64 || D == 128) && BS % 16 == 0 && G <= 64;
+}
+int launch_paged_attention_valu(const PAParams& p, int32_t D, int32_t dtype, int32_t max_q, hipStream_t s,
+                                LaunchLog& log);
 int launch_reshape_and_cache(const void* k, int64_t k_ts, int64_t k_hs, const void* v, int64_t v_ts,
                              int64_t v_hs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs,
                              const int64_t* slots, int64_t T, int64_t num_blocks, int32_t Hkv, int32_t D,

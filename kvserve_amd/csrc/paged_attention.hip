@@ -245,7 +245,6 @@ struct WaveState {
   float m[NT], l[NT];     // m: running max (exp2 domain, -inf when empty); l: lane-partial sum
   int limit[NT];          // keys visible to this lane's row (0 for padding rows)
   float thr[NT], nsh[NT]; // prefill only: raw-score bound that moves m, and -m (0 while m = -inf)
-  f32x4 cinit[NT];        // prefill over pre-scaled Q only: -m in every slot, the QK accumulators' start
 };
 
 // Q rows of tile t: global row r = row0 + 16t + n, valid when r < R.
@@ -406,76 +405,6 @@ __device__ __forceinline__ void pf_lanemax(const f32x4 st[NT][2], float mx[NT]) 
   for (int t = 0; t < NT; ++t)
     mx[t] = fmaxf(fmaxf(fmaxf(st[t][0][0], st[t][0][1]), fmaxf(st[t][0][2], st[t][0][3])),
                   fmaxf(fmaxf(st[t][1][0], st[t][1][1]), fmaxf(st[t][1][2], st[t][1][3])));
-}
-
-// Whether the prefill kernel pre-scales Q: bf16 keeps fp32's exponent range, so q * scale *
-// log2(e) rounded to bf16 cannot overflow (fp16 could, so it keeps the per-score FMA).
-template <class E>
-constexpr bool kPrescaleQ = std::is_same_v<E, BF16>;
-
-// Q of a prefill wave multiplied by scale * log2(e) (sign included) and rounded to E (round to
-// nearest even), so that with accumulators started at -m the QK MFMAs hand back the exp2
-// argument x = q.k scale log2(e) - m itself; the shift starts at 0 with the row empty.
-template <class E, int D, int NT>
-__device__ __forceinline__ void pf_prescale_q(WaveState<D, NT>& s, float cs) {
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-#pragma unroll
-    for (int cc = 0; cc < D / 32; ++cc)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t x = s.q[t][cc][w];
-        s.q[t][cc][w] = E::pack2(__uint_as_float(x << 16) * cs, __uint_as_float(x & 0xffff0000u) * cs);
-      }
-    s.m[t] = 0.f;
-    s.cinit[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-}
-
-// Online-softmax update over pre-scaled Q: st holds x = (scaled score) - m, per-lane maxima of
-// x in mxs. thr is kRescaleSlack, or -inf while the row has seen no key (m = 0 then). When
-// some row of the tile passes it (a uniform branch), each row moves its shift up by its max
-// (the first visible key sets it), x and the start value -m follow, and the accumulators and
-// sums are rescaled; otherwise P = exp2(x) directly (P <= 2^kRescaleSlack).
-template <class E, int D, int NT>
-__device__ __forceinline__ void pf_softmax_pre(WaveState<D, NT>& s, f32x4 st[NT][2], const float mxs[NT],
-                                               u32x4 pt[NT]) {
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    if (__builtin_amdgcn_ballot_w64(mxs[t] > s.thr[t])) {
-      const float mrow = max_over_groups(mxs[t]);  // -inf: no visible key in this chunk
-      const bool empty = s.thr[t] == -INFINITY;
-      const bool still_empty = empty && mrow == -INFINITY;
-      const float d = still_empty ? 0.f : (empty ? mrow : fmaxf(mrow, 0.f));
-      const float alpha = empty ? 1.f : fast_exp2(-d);
-      s.l[t] *= alpha;
-#pragma unroll
-      for (int i = 0; i < D / 16; ++i) s.acc[t][i] *= alpha;
-      s.m[t] += d;
-      s.cinit[t] = f32x4{-s.m[t], -s.m[t], -s.m[t], -s.m[t]};
-      s.thr[t] = still_empty ? -INFINITY : kRescaleSlack;
-#pragma unroll
-      for (int tile = 0; tile < 2; ++tile) st[t][tile] -= d;
-    }
-    float pv[8];
-#pragma unroll
-    for (int tile = 0; tile < 2; ++tile)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) pv[4 * tile + e] = fast_exp2(st[t][tile][e]);
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      pt[t][w] = E::pack2(pv[2 * w], pv[2 * w + 1]);
-      s.l[t] = E::dot2_ones(pt[t][w], s.l[t]);
-    }
-  }
-}
-
-// A row that never saw a key leaves m = -inf (the merge's empty piece), not the shift 0.
-template <int D, int NT>
-__device__ __forceinline__ void pf_prescale_finish(WaveState<D, NT>& s) {
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-    if (s.thr[t] == -INFINITY) s.m[t] = -INFINITY;
 }
 
 // Online-softmax update from (masked) raw scores and per-lane maxima; c > 0 so a -inf
@@ -1120,6 +1049,60 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
   }
 }
 
+// Short decode (plan.short_decode: a decode-only batch of single-tile rows over block tables
+// of at most kShortTokens keys): workgroup (kvh, seq) owns that sequence's rows of kv head kvh.
+// Its 4 waves take chunks w, w + 4, w + 8, ... of the keys, then waves 1-3 hand their online-
+// softmax state to wave 0 through LDS. The accumulator layout is the same in every wave, so
+// the combination is per lane: M = max_w m_w, acc = sum_w 2^(m_w - M) acc_w, and likewise the
+// lane-partial sums; wave 0 then writes the normalised rows. Nothing goes through the
+// workspace and no merge launch follows: a batch this small is bound by latency, and the
+// merge launch was a third of it.
+template <class E, int D, bool KV8>
+__global__ __launch_bounds__(256) void pa_decode_short_kernel(PAParams p) {
+  constexpr int NI = D / 16;
+  __shared__ f32x4 x_acc[kWavesPerWG - 1][NI][64];
+  __shared__ float x_ml[kWavesPerWG - 1][2][64];
+  const int kvh = blockIdx.x, seq = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const SeqView sv = seq_view_uniform(p, seq);
+  if (sv.q_len == 0 || sv.q_len > p.QS) return;  // uniform over the workgroup
+  const int R = sv.q_len * p.G;
+  WaveState<D, 1> st;
+  load_q<D, 1, KV8>(st, p, sv.qs, R, 0, kvh, sv.ctx, sv.kv_total);
+  const int64_t* btrow = p.bt + (int64_t)seq * p.bt_rs;
+  run_chunks<E, D, 1, KV8>(st, p, btrow, kvh, w * kChunk, kWavesPerWG * kChunk, sv.kv_total, sv.kv_total);
+  if (w > 0) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) x_acc[w - 1][i][lane] = st.acc[0][i];
+    x_ml[w - 1][0][lane] = st.m[0];
+    x_ml[w - 1][1][lane] = st.l[0];
+  }
+  __syncthreads();
+  if (w != 0) return;
+  float mw[kWavesPerWG - 1];
+  float M = st.m[0];
+#pragma unroll
+  for (int k = 0; k < kWavesPerWG - 1; ++k) {
+    mw[k] = x_ml[k][0][lane];
+    M = fmaxf(M, mw[k]);
+  }
+  const float ms = M == -INFINITY ? 0.f : M;  // no key seen by any wave: every weight is 0
+  const float a0 = fast_exp2(st.m[0] - ms);
+  st.l[0] *= a0;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) st.acc[0][i] *= a0;
+#pragma unroll
+  for (int k = 0; k < kWavesPerWG - 1; ++k) {
+    const float ak = fast_exp2(mw[k] - ms);
+    st.l[0] += ak * x_ml[k][1][lane];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) st.acc[0][i] += ak * x_acc[k][i][lane];
+  }
+  st.m[0] = M;
+  write_rows<E, D, 1>(st, p, sv, R, 0, kvh, false, nullptr, nullptr, 0);
+}
+
 // Log-sum-exp merge of split segments. A job covers `rows` partial rows per piece (HGW
 // heads x RS rows for decode, PAParams::PR rows of one head for prefill); row x of piece i
 // sits at (slot(i) * rows + x) in the partial arrays. Each workgroup merges MR = 1024 / D
@@ -1475,7 +1458,7 @@ __device__ __forceinline__ void pf_k_lanes(uint32_t ka[D / 32], const char* lds)
 }
 
 // S^T of one chunk from the K stage, one 16-key tile at a time (16 registers of K operands
-// live instead of 32). Over pre-scaled Q the accumulators start at -m (the exp2 argument).
+// live instead of 32).
 template <class E, int D, int NT>
 __device__ __forceinline__ void pf_scores_lds(const WaveState<D, NT>& s, const uint32_t ka[D / 32], int stage,
                                               f32x4 st[NT][2]) {
@@ -1489,7 +1472,7 @@ __device__ __forceinline__ void pf_scores_lds(const WaveState<D, NT>& s, const u
       k[cc] = *(lds_u32x4_ptr)(uintptr_t)(ka[cc] + (uint32_t)(stage + tile * L::kKHalfBytes));
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      f32x4 a = kPrescaleQ<E> ? s.cinit[t] : f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int cc = 0; cc < D / 32; ++cc) a = E::mfma(k[cc], s.q[t][cc], a);
       st[t][tile] = a;
@@ -1656,16 +1639,15 @@ struct PfPriority {
   }
 };
 
-// The query tile as the score MFMAs take it, and the exp2 argument's factor c: over bf16, Q
-// pre-scaled by scale log2(e) (c unused); otherwise the exp2 argument is fma(score, c, -m)
-// with c > 0: for a negative scale S c = (-Q) K^T |c| (a sign flip of Q is exact), for a
-// zero scale every score is 0 = (0 Q) K^T 1.
+// The query tile as the score MFMAs take it, and the exp2 argument's factor c > 0: the
+// argument is fma(score, c, -m) in fp32 (the scale is never rounded into a 16-bit Q, whose
+// rounding would move large scores by up to 2^-9 of their size); for a negative scale
+// S c = (-Q) K^T |c| (a sign flip of Q is exact), for a zero scale every score is
+// 0 = (0 Q) K^T 1.
 template <class E, int D, int NT>
 __device__ __forceinline__ float pf_q_ready(WaveState<D, NT>& s, const PAParams& p) {
   float c = fabsf(p.qk_scale);
-  if constexpr (kPrescaleQ<E>) {
-    pf_prescale_q<E, D, NT>(s, p.qk_scale);
-  } else if (p.qk_scale < 0.f) {
+  if (p.qk_scale < 0.f) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -1784,10 +1766,7 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
     pf_v_issue<D, SOFF + L::kKBytes, 0, kVLead>(vt, vb);
     __builtin_amdgcn_sched_barrier(0);
     u32x4 pt[NT];
-    if constexpr (kPrescaleQ<E>)
-      pf_softmax_pre<E, D, NT>(s, sc, mx, pt);
-    else
-      pf_softmax<E, D, NT>(s, sc, mx, c, pt);
+    pf_softmax<E, D, NT>(s, sc, mx, c, pt);
     pf_pv<E, D, NT, MASKED, SOFF + L::kKBytes>(s, vt, vb, cr, sv.kv_total, pt);
   };
   using S0 = std::integral_constant<int, 0>;
@@ -1817,7 +1796,6 @@ __device__ __forceinline__ void prefill_tile(char* lds, const PAParams& p, const
     sync(i, next * L::kStageBytes);
     stg = stg == 2 ? 0 : stg + 1;
   }
-  if constexpr (kPrescaleQ<E>) pf_prescale_finish<D, NT>(s);
   pf_write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, slot * PRW - wg_row0);
 }
 
@@ -1943,10 +1921,7 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
     pf_v_issue<D, SOFF + L::kKBytes, 0, kVLead>(vt, vb);
     __builtin_amdgcn_sched_barrier(0);
     u32x4 pt[NT];
-    if constexpr (kPrescaleQ<E>)
-      pf_softmax_pre<E, D, NT>(s, sc, mx, pt);
-    else
-      pf_softmax<E, D, NT>(s, sc, mx, c, pt);
+    pf_softmax<E, D, NT>(s, sc, mx, c, pt);
     pf_pv<E, D, NT, MASKED, SOFF + L::kKBytes>(s, vt, vb, cr, sv.kv_total, pt);
   };
   using I0 = std::integral_constant<int, 0>;
@@ -1969,7 +1944,6 @@ __device__ __forceinline__ void prefill_tile_kv8(char* lds, const PAParams& p, c
       sync(i, I0{});
     if (i < n_my) compute(i, (i & 1) * L::kStageBytes, S0{}, std::true_type{});
   }
-  if constexpr (kPrescaleQ<E>) pf_prescale_finish<D, NT>(s);
   pf_write_rows<E, D, NT>(s, p, sv, R, row0, kvh, partial, slot * PRW - wg_row0);
 }
 
@@ -2258,6 +2232,12 @@ static int launch_decode_nt(PAParams& p, hipStream_t s) {
 template <class E, int D, bool KV8>
 static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipStream_t s, LaunchLog& log) {
   int err = 0;
+  if (plan.short_decode) {
+    hipLaunchKernelGGL((pa_decode_short_kernel<E, D, KV8>), dim3(p.Hkv, p.B), dim3(256), 0, s, p);
+    if ((err = (int)hipGetLastError())) return err;
+    log.after_launch(1, s);
+    return 0;
+  }
   p.PLAN = plan.launch_prefill ? 1 : 0;
   p.CASC = plan.cascade ? 1 : 0;
   if (plan.cascade) {

@@ -178,7 +178,7 @@ class PagedLlama:
     interface (`write_kv` / `forward`, src/kvserve/attention.py:39-102)."""
 
     def __init__(self, cfg: ModelConfig, weights: Weights, backend=HipAttention, max_positions: int = 4096,
-                 fused_ops: bool | None = None):  # fmt: skip
+                 fused_ops: bool | None = None, fused_rope: bool | None = None):  # fmt: skip
         self.cfg = cfg
         self.w = weights
         self.backend = backend
@@ -188,9 +188,14 @@ class PagedLlama:
         self.scale = cfg.head_dim**-0.5
         self.q_width = cfg.num_heads * cfg.head_dim
         self.kv_width = cfg.num_kv_heads * cfg.head_dim
-        # what the backend offers beyond write_kv / forward
-        self.fused_rope = callable(getattr(backend, "rope_and_cache", None))
-        self.fused_projection = callable(getattr(backend, "gemv_rope_and_cache", None))
+        # What the backend offers beyond write_kv / forward. fused_rope=False drives it exactly
+        # as kvserve's Attention.attend does (src/kvserve/model.py:84-108): split + RoPE in
+        # torch, write_kv with v a strided view of the fused QKV output, then forward(out=...).
+        offered = callable(getattr(backend, "rope_and_cache", None))
+        if fused_rope and not offered:
+            raise ValueError("the backend has no fused RoPE + cache write (rope_and_cache)")
+        self.fused_rope = offered if fused_rope is None else bool(fused_rope)
+        self.fused_projection = self.fused_rope and callable(getattr(backend, "gemv_rope_and_cache", None))
         probe = torch.empty(0, dtype=self.dtype, device=self.device)
         self.fused_ops = ops.enabled(probe) if fused_ops is None else bool(fused_ops)
         if self.fused_ops and not ops.enabled(probe):
@@ -294,11 +299,12 @@ class PagedLlama:
 
 def build_model(cfg: ModelConfig, device, dtype: torch.dtype, max_positions: int, backend=HipAttention,
                 weights: Path | None = None, seed: int = 0, std: float = 0.02,
-                fused_ops: bool | None = None) -> PagedLlama:  # fmt: skip
+                fused_ops: bool | None = None, fused_rope: bool | None = None) -> PagedLlama:  # fmt: skip
     """A PagedLlama on `device` in `dtype`: weights from a Hugging Face safetensors directory,
     else synthetic (`random_weights`). fused_ops (default: on a GPU with 16-bit weights) selects
-    libkvhip's layer kernels for the row-wise work."""
+    libkvhip's layer kernels for the row-wise work; fused_rope=False keeps the backend to
+    kvserve's write_kv + forward calls (default: its fused RoPE + cache write when offered)."""
     device = torch.device(device)
     w = load_hf_weights(weights, cfg, device, dtype) if weights is not None else random_weights(cfg, device, dtype,
                                                                                                  seed, std)  # fmt: skip
-    return PagedLlama(cfg, w, backend, max_positions, fused_ops)
+    return PagedLlama(cfg, w, backend, max_positions, fused_ops, fused_rope)

@@ -296,6 +296,9 @@ class ModelRunner:
                  piecewise_graphs: bool | None = None, max_graph_batch: int = 128, max_piecewise_tokens: int = 512,
                  token_budget: int = 2048, device_metadata: bool | None = None, max_seqs: int = 1024,
                  kv_cache_dtype: torch.dtype | None = None):  # fmt: skip
+        if max_model_len > model.max_positions:
+            # positions past the RoPE tables would be clamped (fused kernel) or index out of range
+            raise ValueError(f"max_model_len {max_model_len} exceeds the model's {model.max_positions} RoPE positions")
         self.model = model
         self.device = model.device
         self.block_size, self.max_model_len = block_size, max_model_len

@@ -162,6 +162,16 @@ def test_pool_sized_from_gib(hf_checkpoint):
     assert r.kv_caches.shape == (2, 2, r.pool.num_blocks + 1, 16, 2, 16)
 
 
+def test_max_model_len_is_bounded_by_the_rope_tables(hf_checkpoint):
+    """Positions past the model's RoPE tables would be clamped or index out of range: the runner
+    refuses a max_model_len above max_positions (the reference builds the model with
+    max_positions = max_model_len, model_runner.py:29)."""
+    _, path = hf_checkpoint
+    with pytest.raises(ValueError, match="RoPE positions"):
+        ModelRunner(_ours(path, max_pos=512), num_blocks=8, block_size=16, max_model_len=513)
+    assert ModelRunner(_ours(path, max_pos=512), num_blocks=8, block_size=16, max_model_len=512).max_model_len == 512
+
+
 def test_torch_backend_runs_without_graphs(hf_checkpoint):
     _, path = hf_checkpoint
     r = _runner(path)

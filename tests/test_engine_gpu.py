@@ -5,6 +5,9 @@ backend (the reference's tests/test_engine.py:85-94), including 5-token budgets 
 prefill chunks with decodes, and the graph paths (decode graphs, piecewise graphs with eager
 attention between them) give the eager path's tokens on mixed steps with staggered arrivals
 (tests/test_cuda_graph.py:41-58, 112-158 of the reference), with every step on a graph path.
+Each of these runs twice: with the backend's fused RoPE + cache write, and with the model
+driving the backend exactly as kvserve's Attention.attend does (src/kvserve/model.py:84-108:
+torch RoPE, write_kv with v a strided view of the fused QKV output, forward(out=...)).
 
 bf16 (the MFMA, stream-K and merge kernels): teacher-forced against the torch backend, so both
 see the same tokens; logits agree within 5% of their scale at every step and at least 90% of
@@ -12,6 +15,8 @@ the greedy picks agree (bf16 near-ties may flip, as the reference notes, README.
 """
 
 from __future__ import annotations
+
+from collections import Counter
 
 import pytest
 import torch
@@ -32,22 +37,74 @@ SMALL = ModelConfig(
 PROMPTS = [[(31 * i + 7) % 2048 for i in range(n)] for n in (5, 37, 130, 16)]
 
 
-def _model(backend, dtype, cfg=SMALL, std=0.06):
-    return build_model(cfg, "cuda:0", dtype, 1024, backend=backend, seed=1234, std=std)
+class CountingHip(HipAttention):
+    """HipAttention with its entry points counted, and whether write_kv saw a strided v."""
+
+    calls: Counter = Counter()
+
+    @staticmethod
+    def write_kv(k_cache, v_cache, k, v, slots, **kw):
+        CountingHip.calls["write_kv"] += 1
+        CountingHip.calls["strided_v"] += int(not v.is_contiguous())
+        return HipAttention.write_kv(k_cache, v_cache, k, v, slots, **kw)
+
+    @staticmethod
+    def forward(q, k_cache, v_cache, meta, scale, out=None, **kw):
+        CountingHip.calls["forward"] += 1
+        CountingHip.calls["forward_out"] += int(out is not None)
+        return HipAttention.forward(q, k_cache, v_cache, meta, scale, out=out, **kw)
+
+    @staticmethod
+    def rope_and_cache(*a, **kw):
+        CountingHip.calls["rope_and_cache"] += 1
+        return HipAttention.rope_and_cache(*a, **kw)
+
+    @staticmethod
+    def gemv_rope_and_cache(*a, **kw):
+        CountingHip.calls["gemv_rope_and_cache"] += 1
+        return HipAttention.gemv_rope_and_cache(*a, **kw)
+
+
+def _hip(fused_rope):
+    """The HIP backend for one variant of a test: fused (None) or kvserve's unfused calls
+    (False, counted)."""
+    CountingHip.calls.clear()
+    return HipAttention if fused_rope is None else CountingHip
+
+
+def _check_unfused_calls(fused_rope) -> None:
+    """The unfused variant called write_kv (v strided: a view of the fused QKV output, except
+    where a one-token view counts as contiguous) and forward only."""
+    if fused_rope is None:
+        return
+    c = CountingHip.calls
+    assert c["write_kv"] > 0 and c["strided_v"] > 0 and c["forward"] > 0, c
+    assert c["rope_and_cache"] == 0 and c["gemv_rope_and_cache"] == 0, c
+
+
+FUSED = pytest.mark.parametrize("fused_rope", [None, False], ids=["fused", "write_kv+forward"])
+
+
+def _model(backend, dtype, cfg=SMALL, std=0.06, fused_rope=None):
+    return build_model(cfg, "cuda:0", dtype, 1024, backend=backend, seed=1234, std=std, fused_rope=fused_rope)
 
 
 def _runner(backend, dtype, **kw):
     kw.setdefault("num_blocks", 128)
-    return ModelRunner(_model(backend, dtype, kw.pop("cfg", SMALL), kw.pop("std", 0.06)), max_model_len=1024, **kw)
+    model = _model(backend, dtype, kw.pop("cfg", SMALL), kw.pop("std", 0.06), kw.pop("fused_rope", None))
+    return ModelRunner(model, max_model_len=1024, **kw)
 
 
-def test_fp32_greedy_tokens_identical_to_torch_backend(hip_device):
+@FUSED
+def test_fp32_greedy_tokens_identical_to_torch_backend(hip_device, fused_rope):
     want = generate(_runner(TorchRefAttention, torch.float32), PROMPTS, 24)
-    eager = _runner(HipAttention, torch.float32, decode_graphs=False, piecewise_graphs=False)
+    hip = _hip(fused_rope)
+    eager = _runner(hip, torch.float32, decode_graphs=False, piecewise_graphs=False, fused_rope=fused_rope)
     assert generate(eager, PROMPTS, 24) == want
-    graphs = _runner(HipAttention, torch.float32, max_graph_batch=8)
+    graphs = _runner(hip, torch.float32, max_graph_batch=8, fused_rope=fused_rope)
     assert generate(graphs, PROMPTS, 24) == want
     assert graphs.paths["decode_graph"] == 23 and graphs.paths["piecewise"] == 1, graphs.paths  # 188-token prefill
+    _check_unfused_calls(fused_rope)
 
 
 def _staggered(runner: ModelRunner, prompts, max_new: int, budget: int, forced=None) -> list[list[int]]:
@@ -87,27 +144,37 @@ def _logits_spy(runner: ModelRunner) -> list[torch.Tensor]:
     return logs
 
 
-def test_fp32_five_token_budget_identical_to_torch_backend(hip_device):
+@FUSED
+def test_fp32_five_token_budget_identical_to_torch_backend(hip_device, fused_rope):
     """Every prompt is chunked into 5-token steps that also carry the other sequences' decode
-    tokens; HIP with both graph modes gives the torch backend's tokens."""
+    tokens; HIP with both graph modes gives the torch backend's tokens (the reference's
+    tests/test_engine.py:86-93)."""
     prompts = [p[:23] for p in PROMPTS]
     want = _staggered(_runner(TorchRefAttention, torch.float32), prompts, 10, budget=5)
-    hip = _runner(HipAttention, torch.float32, max_graph_batch=8, token_budget=5)
+    hip = _runner(_hip(fused_rope), torch.float32, max_graph_batch=8, token_budget=5, fused_rope=fused_rope)
     assert _staggered(hip, prompts, 10, budget=5) == want
     assert hip.paths["piecewise"] > 0 and hip.paths["decode_graph"] > 0 and hip.paths["eager"] == 0, hip.paths
+    _check_unfused_calls(fused_rope)
+    if fused_rope is not None:  # the piecewise steps' attention wrote into the static buffer
+        assert CountingHip.calls["forward_out"] > 0, CountingHip.calls
 
 
-def test_piecewise_matches_eager_on_mixed_steps(hip_device):
+@FUSED
+def test_piecewise_matches_eager_on_mixed_steps(hip_device, fused_rope):
     """A 24-token budget forces chunked prefills mixed with decodes; with graphs every step goes
-    through a graph path and the tokens equal eager execution's."""
+    through a graph path and the tokens equal eager execution's (the reference's
+    tests/test_cuda_graph.py:112-135)."""
     prompts = [p * 3 for p in PROMPTS[:3]] + [PROMPTS[3]]
-    eager = _runner(HipAttention, torch.float32, decode_graphs=False, piecewise_graphs=False, token_budget=24)
+    hip = _hip(fused_rope)
+    eager = _runner(hip, torch.float32, decode_graphs=False, piecewise_graphs=False, token_budget=24,
+                    fused_rope=fused_rope)  # fmt: skip
     want = _staggered(eager, prompts, 12, budget=24)
     assert set(eager.paths) == {"eager"}
-    g = _runner(HipAttention, torch.float32, max_graph_batch=8, token_budget=24)
+    g = _runner(hip, torch.float32, max_graph_batch=8, token_budget=24, fused_rope=fused_rope)
     assert g.piecewise.max_tokens == 24  # capped by the step budget
     assert _staggered(g, prompts, 12, budget=24) == want
     assert g.paths["piecewise"] > 0 and g.paths["decode_graph"] > 0 and g.paths["eager"] == 0, g.paths
+    _check_unfused_calls(fused_rope)
 
 
 def test_large_steps_bypass_piecewise(hip_device):
@@ -211,7 +278,8 @@ def test_batched_generation_equals_one_sequence_at_a_time(hip_device):
     assert together == alone
 
 
-def test_bf16_llama_1b_shape_tracks_the_torch_backend(hip_device):
+@FUSED
+def test_bf16_llama_1b_shape_tracks_the_torch_backend(hip_device, fused_rope):
     """The Llama-3.2-1B layer shapes (32 q / 8 kv heads, D 64) in bf16 with two layers, a
     48-token budget so prompts are chunked into mixed steps, graphs on: teacher-forced against
     the torch backend, logits within 5% of their scale at every step, >= 90% greedy agreement."""
@@ -220,7 +288,8 @@ def test_bf16_llama_1b_shape_tracks_the_torch_backend(hip_device):
     ref = _runner(TorchRefAttention, torch.bfloat16, cfg=cfg, std=0.03, num_blocks=64)
     l_ref = _logits_spy(ref)
     forced = _staggered(ref, prompts, 12, budget=48)
-    hip = _runner(HipAttention, torch.bfloat16, cfg=cfg, std=0.03, num_blocks=64, max_graph_batch=4, token_budget=48)
+    hip = _runner(_hip(fused_rope), torch.bfloat16, cfg=cfg, std=0.03, num_blocks=64, max_graph_batch=4,
+                  token_budget=48, fused_rope=fused_rope)  # fmt: skip
     l_hip = _logits_spy(hip)
     assert _staggered(hip, prompts, 12, budget=48, forced=forced) == forced
     assert len(l_ref) == len(l_hip) and hip.paths["piecewise"] > 0 and hip.paths["decode_graph"] > 0, hip.paths
@@ -232,6 +301,7 @@ def test_bf16_llama_1b_shape_tracks_the_torch_backend(hip_device):
         total += a.shape[0]
     print(f"bf16 greedy agreement HIP vs torch backend (teacher-forced): {agree}/{total}")
     assert agree >= 0.9 * total, (agree, total)
+    _check_unfused_calls(fused_rope)
 
 
 def test_device_metadata_runner_matches_host_metadata_runner(hip_device):

@@ -111,12 +111,12 @@ def test_reshape_and_cache_fp8_rejects_bad_arguments(lib, over, status):
 
 def _pa8(lib, **over):
     a = dict(q=0x1000, kcs=(16 * 1024, 1024, 128), vcs=(16 * 1024, 1024, 128), ks=1.0, vs=1.0, dtype=2, ws=0,
-             ws_bytes=0)  # fmt: skip
+             ws_bytes=0, D=128, BS=16)  # fmt: skip
     a.update(over)
     return lib.kvh_paged_attention_fp8(
         a["q"], 32 * 128, 128, 0x2000, _lib.i64x3(a["kcs"]), 0x3000, _lib.i64x3(a["vcs"]), 64, 0x4000, 32 * 128, 128,
-        0x5000, 64, 64, 0x6000, 0x7000, 8, 8, 32, 8, 128, 16, 1, 128**-0.5, a["ks"], a["vs"], a["dtype"], a["ws"],
-        a["ws_bytes"], None,
+        0x5000, 128, 128, 0x6000, 0x7000, 8, 8, 32, 8, a["D"], a["BS"], 1, 128**-0.5, a["ks"], a["vs"], a["dtype"],
+        a["ws"], a["ws_bytes"], None,
     )  # fmt: skip
 
 
@@ -124,6 +124,8 @@ def _pa8(lib, **over):
     "over,status",
     [
         (dict(dtype=0), E_UNSUPPORTED),  # fp32 queries have no E4M3 path
+        (dict(D=96), E_UNSUPPORTED),  # E4M3 caches feed the MFMA kernels only: D 64 / 128,
+        (dict(BS=8), E_UNSUPPORTED),  # pages of whole 16-token tiles
         (dict(ks=0.0), E_SHAPE),
         (dict(vs=math.inf), E_SHAPE),
         (dict(kcs=(16 * 1024, 1024, 8)), E_ALIGN),  # E4M3 rows are read 16 bytes at a time

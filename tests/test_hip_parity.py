@@ -81,6 +81,60 @@ def test_fp32_any_block_size(hip_device):
     assert pc.max_err_vs_oracle(b, out, [0, 1, 2]) <= pc.TOL_F32
 
 
+@pytest.mark.parametrize("kind", ["q_x8", "outlier_channels"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_sharp_softmax_large_scores(hip_device, kind, dtype):
+    """Large scores (a sharp softmax, as attention sinks and outlier channels give real models):
+    q scaled by 8 (scores up to ~50 in log2 units), or four channels of q and of every key
+    scaled by 16 and 4. Decode, verify and prefill rows (the stream-K decode and the prefill
+    kernel) against the fp64 oracle at the 16-bit tolerance: the softmax scale is applied in
+    fp32, never rounded into a 16-bit operand."""
+    w = workloads.custom("sharp", [1, 5, 384, 200, 1], [2000, 1500, 1000, 0, 3000], 32, 8, 128, 16, seed=21)
+    b = workloads.materialize(w, dtype, hip_device, seed=21)
+    if kind == "q_x8":
+        b.q.mul_(8)
+    else:
+        b.q[..., :4] *= 16
+        b.k_new[..., :4] *= 4
+        b.k_cache[..., :4] *= 4
+    out = pc.attend(b)
+    assert "prefill" in last_launch_kernels()
+    err = pc.max_err_vs_oracle(b, out, list(range(len(w.query_lens))), rows_per_seq=64)
+    assert err <= pc.TOL_16BIT, f"{kind} {dtype}: max abs err {err}"
+
+
+@pytest.mark.parametrize("case", list(workloads.REFERENCE_CASES))
+@pytest.mark.parametrize("head_dim", [32, 80, 96, 256])
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_head_sizes_outside_the_mfma_tiles(hip_device, case, head_dim, dtype):
+    """Head sizes other than 64 and 128 (the reference pads any head size to a power of two and
+    masks it, kernels/paged_attention.py:64-67,154) run on the vector-ALU kernel: the
+    reference's CASES against the torch oracle at the 16-bit tolerance."""
+    w = workloads.reference_case(case, 32, 8, head_dim=head_dim, block_size=16, seed=3)
+    b = workloads.materialize(w, dtype, hip_device, seed=3)
+    out = pc.attend(b)
+    assert last_launch_kernels() == ["valu16"]
+    assert pc.written_rows_match(b)
+    err = (out.float().cpu() - pc.torch_oracle_full(b)).abs().max().item()
+    assert err <= pc.TOL_16BIT, f"{case} D={head_dim} {dtype}: max abs err {err}"
+
+
+@pytest.mark.parametrize(
+    "heads,block_size",
+    [((32, 8), 8), ((32, 8), 24), ((128, 1), 16)],
+    ids=["bs8", "bs24", "g128"],
+)
+def test_pages_and_groups_outside_the_mfma_tiles(hip_device, heads, block_size):
+    """Pages that are not whole 16-token tiles, and GQA groups above 64 query heads, run on the
+    vector-ALU kernel at D = 128: decode, verify and prefill rows against the torch oracle."""
+    w = workloads.custom("odd_pages", [1, 5, 37, 1], [300, 64, 100, 0], *heads, 128, block_size, seed=4)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=4)
+    out = pc.attend(b)
+    assert last_launch_kernels() == ["valu16"]
+    err = (out.float().cpu() - pc.torch_oracle_full(b)).abs().max().item()
+    assert err <= pc.TOL_16BIT, f"{heads} BS={block_size}: {err}"
+
+
 @pytest.mark.parametrize("idx", [1, 2, 3, 4, 5])
 def test_baseline_configs(hip_device, idx):
     """BASELINE configs at full size: write + attend, then the fp64 oracle on sampled
@@ -156,6 +210,31 @@ def test_stale_slots_and_columns_never_read(hip_device):
     out = pc.attend(b)
     assert torch.isfinite(out.float()).all()
     assert pc.max_err_vs_oracle(b, out, [0, 1, 2, 3]) <= pc.TOL_16BIT
+
+
+@pytest.mark.parametrize("heads", [(32, 8), (16, 16), (32, 2), (64, 4)], ids=lambda h: f"{h[0]}q{h[1]}kv")
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_short_tables_take_the_single_launch_decode(hip_device, heads, head_dim, dtype):
+    """Decode batches over block tables of at most 1024 keys (the 1B decode config's shape) run
+    one launch: a workgroup per (sequence, kv head) whose 4 waves split the chunks and combine
+    their partials in LDS. Contexts from 0 to the table's end, so some waves see no chunk.
+    Against the torch oracle, and against the stream-K kernels + merge on the same batch seen
+    through a table 4x wider (within accumulation rounding)."""
+    ctx = [0, 1, 31, 32, 33, 95, 96, 200, 511, 1023]
+    w = workloads.custom("short", [1] * len(ctx), ctx, *heads, head_dim, 16, seed=13)
+    b = workloads.materialize(w, dtype, hip_device, seed=13)
+    assert b.meta.block_tables.shape[1] == 64
+    out = pc.attend(b)
+    assert last_launch_kernels() == ["decode"]
+    err = (out.float().cpu() - pc.torch_oracle_full(b)).abs().max().item()
+    assert err <= pc.TOL_16BIT, f"{heads} D={head_dim}: {err}"
+    bt = torch.zeros(len(ctx), 256, dtype=torch.long, device=hip_device)
+    bt[:, :64] = b.meta.block_tables
+    b.meta.block_tables = bt
+    wide = HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale)
+    assert "reduce" in last_launch_kernels()
+    assert (out.float() - wide.float()).abs().max().item() <= 1e-2
 
 
 def test_split_k_matches_single_pass(hip_device):
@@ -260,9 +339,11 @@ def test_argument_errors_raise(hip_device):
     b = workloads.materialize(w, torch.bfloat16, hip_device)
     with pytest.raises(ValueError):
         HipAttention.forward(b.q.float(), b.k_cache, b.v_cache, b.meta, w.scale)
-    bad = torch.empty(b.k_cache.shape[:3] + (96,), dtype=torch.bfloat16, device=hip_device)
-    with pytest.raises((ValueError, RuntimeError)):
-        HipAttention.forward(b.q[..., :96].contiguous(), bad, bad, b.meta, w.scale)
+    for d in (100, 264):  # head sizes no kernel computes: not whole 16-byte rows, past 256
+        bad = torch.empty(b.k_cache.shape[:3] + (d,), dtype=torch.bfloat16, device=hip_device)
+        q = torch.empty(b.q.shape[:2] + (d,), dtype=torch.bfloat16, device=hip_device)
+        with pytest.raises((ValueError, RuntimeError)):
+            HipAttention.forward(q, bad, bad, b.meta, w.scale)
 
 
 @pytest.mark.parametrize("block_size", [32, 64])
@@ -322,6 +403,10 @@ def test_auto_selector_on_the_device(hip_device):
             get_backend("hip", hip_device, bs)
     assert get_backend("auto", "cpu", 16, fallback) is fallback
     assert get_backend("auto", hip_device, 8) is None
+    # a head size the MFMA kernels do not take keeps the caller's choice under "auto"
+    assert get_backend("auto", hip_device, 16, fallback, head_dim=96) is fallback
+    assert get_backend("auto", hip_device, 16, fallback, head_dim=128) is HipAttention
+    assert get_backend("hip", hip_device, 16, head_dim=96) is HipAttention
 
 
 @pytest.mark.parametrize("layout", ["padded_rows", "head_major"])
@@ -369,23 +454,39 @@ def test_strided_cache_layouts(hip_device, layout, fp8):
         assert pc.max_err_vs_oracle(b, ref, list(range(len(w.query_lens)))) <= pc.TOL_16BIT
 
 
-def test_prefill_page_outside_the_pool_after_the_first_window(hip_device):
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "e4m3"])
+def test_prefill_page_outside_the_pool_after_the_first_window(hip_device, fp8):
     """A block-table entry outside the pool is a missing page: its 16 keys take no part in
     the softmax (the prefill kernel reads block 0 for it and masks the keys). Placed past the
     first 64 chunks of long stream-K pieces (8 x 2048 queries over 2048 cached tokens), it
-    also pins that a page-window refresh extends the unmasked run only up to such a page.
-    Expected rows are computed here in fp64 from the cache without those keys."""
+    also pins that a page-window refresh extends the unmasked run only up to such a page, in
+    the 16-bit tile and in the E4M3 tile (scales 0.5 / 0.25). Expected rows are computed here
+    in fp64 from the (dequantized) cache without those keys."""
+    from oracle import fp8 as fp8_oracle
+
     H, Hkv, D, BS = 32, 8, 128, 16
     w = workloads.custom("missing_page", [2048] * 8, [2048] * 8, H, Hkv, D, BS, seed=11)
     b = workloads.materialize(w, torch.bfloat16, hip_device, seed=11)
     seq, page = 3, 200  # tokens 3200 .. 3215 of sequence 3
     b.meta.block_tables[seq, page] = w.num_blocks + 7
-    out = pc.attend(b)
+    if fp8:
+        ks, vs = 0.5, 0.25
+        kc8 = fp8_oracle.quantize(b.k_cache, ks).to(hip_device)
+        vc8 = fp8_oracle.quantize(b.v_cache, vs).to(hip_device)
+        HipAttention.write_kv(kc8, vc8, b.k_new, b.v_new, b.meta.slot_mapping, k_scale=ks, v_scale=vs)
+        out = HipAttention.forward(b.q, kc8, vc8, b.meta, w.scale, k_scale=ks, v_scale=vs)
+    else:
+        out = pc.attend(b)
     assert "prefill" in last_launch_kernels()
     G, ctx, q0 = H // Hkv, w.seq_lens[seq] - w.query_lens[seq], sum(w.query_lens[:seq])
     table = torch.tensor(w.tables[seq], dtype=torch.long, device=hip_device)
-    kc = b.k_cache.index_select(0, table).to(torch.float64).cpu().reshape(-1, Hkv, D).numpy()
-    vc = b.v_cache.index_select(0, table).to(torch.float64).cpu().reshape(-1, Hkv, D).numpy()
+    if fp8:
+        kc = fp8_oracle.dequantize(kc8.index_select(0, table).cpu(), ks).to(torch.float64)
+        vc = fp8_oracle.dequantize(vc8.index_select(0, table).cpu(), vs).to(torch.float64)
+        kc, vc = kc.reshape(-1, Hkv, D).numpy(), vc.reshape(-1, Hkv, D).numpy()
+    else:
+        kc = b.k_cache.index_select(0, table).to(torch.float64).cpu().reshape(-1, Hkv, D).numpy()
+        vc = b.v_cache.index_select(0, table).to(torch.float64).cpu().reshape(-1, Hkv, D).numpy()
     keep = np.ones(kc.shape[0], dtype=bool)
     keep[page * BS : (page + 1) * BS] = False
     err = 0.0

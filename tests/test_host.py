@@ -70,8 +70,8 @@ def _call(lib, a):
     [
         (dict(dtype=7), E_DTYPE),
         (dict(H=30), E_SHAPE),
-        (dict(D=96), E_UNSUPPORTED),
-        (dict(BS=8), E_UNSUPPORTED),
+        (dict(D=100), E_UNSUPPORTED),  # 16-bit rows of whole 16-byte vectors only
+        (dict(D=264), E_UNSUPPORTED),  # the vector-ALU kernel's query row holds 256
         (dict(Hkv=0), E_SHAPE),
         (dict(W=0), E_SHAPE),
         (dict(q=0), E_NULL),
@@ -170,11 +170,16 @@ def test_workspace_follows_the_plan(lib):
         plan = up(32) + up(B * 4) + up((B + 1) * 8) + up(768 * 64) if prefill else 0
         return up(rows * D * 4) + up(rows * 2 * 4) + up(jobs * 16 * 4) + up(prows * D * 4) + up(prows * 2 * 4) + plan
 
-    assert ws(8, 8, 32, 8, 64, 32, 16, 1, 2) == want(8, 8, 4, 1, 64)  # C1
+    # C1: tables of at most 1024 keys take the short decode (one workgroup per sequence and kv
+    # head, partials combined in LDS): no workspace
+    assert ws(8, 8, 32, 8, 64, 32, 16, 1, 2) == 0
+    assert ws(8, 8, 32, 8, 64, 64, 16, 1, 2) == 0
+    assert ws(8, 8, 32, 8, 64, 65, 16, 1, 2) == want(8, 8, 4, 1, 64)
+    assert ws(8, 8, 32, 8, 64, 32, 16, 5, 2) == want(8, 8, 4, 5, 64)  # verify rows: two tiles, stream-K
     assert ws(64, 64, 32, 8, 128, 512, 16, 1, 2) == want(64, 8, 4, 1, 128)  # C2
     assert ws(160, 32, 32, 8, 128, 257, 16, 5, 2) == want(32, 8, 4, 5, 128)  # C5: verify rows
     assert ws(2048, 516, 32, 8, 128, 280, 16, 384, 2) == want(516, 8, 4, 4, 128, prefill=True)  # C3
-    assert ws(8, 8, 16, 2, 64, 32, 16, 1, 2) == want(8, 2, 8, 1, 64, hgw=2)  # two kv heads
+    assert ws(8, 8, 16, 2, 64, 128, 16, 1, 2) == want(8, 2, 8, 1, 64, hgw=2)  # two kv heads
     assert ws(64, 64, 32, 8, 128, 512, 16, 1, 0) == 0  # fp32 path: no split
     assert ws(64, 64, 30, 8, 128, 512, 16, 1, 2) == 0  # invalid shape
 
@@ -203,6 +208,18 @@ def test_get_backend_contract(monkeypatch):
         with pytest.raises(ValueError):
             attention.get_backend("hip", "cuda", bs)
     assert attention.get_backend("auto", "cpu", 16, fallback=fallback) is fallback
+    # head sizes: "auto" keeps the caller's choice unless the MFMA kernels take the heads;
+    # "hip" computes any multiple of 8 up to 256 and rejects the rest
+    for d in (64, 128):
+        assert attention.get_backend("auto", "cuda", 16, fallback=fallback, head_dim=d) is attention.HipAttention
+        assert attention.get_backend("hip", "cuda", 16, head_dim=d) is attention.HipAttention
+    for d in (32, 80, 96, 256):
+        assert attention.get_backend("auto", "cuda", 16, fallback=fallback, head_dim=d) is fallback
+        assert attention.get_backend("hip", "cuda", 16, head_dim=d) is attention.HipAttention
+    for d in (100, 264, 0):
+        assert attention.get_backend("auto", "cuda", 16, fallback=fallback, head_dim=d) is fallback
+        with pytest.raises(ValueError):
+            attention.get_backend("hip", "cuda", 16, head_dim=d)
     cls = attention.HipAttention
     assert cls.graph_capturable and not cls.needs_padded_layout
 
@@ -486,7 +503,8 @@ def test_isa_check_joins_take_the_weaker_state():
 def test_built_kernels_have_no_partial_exec_spills():
     from kvserve_amd import isa_check
 
-    asms = sorted((Path(__file__).resolve().parents[1] / "kvserve_amd" / "_build").glob("*.gfx950.s"))
+    # the device assembly each object was assembled from (kept by the build's -save-temps)
+    asms = sorted((Path(__file__).resolve().parents[1] / "kvserve_amd" / "_build").glob("*-hip-amdgcn-amd-amdhsa-gfx950.s"))
     if not asms:
         pytest.skip("no device assembly: run python -m kvserve_amd.build")
     assert [hit for a in asms for hit in isa_check.check(a.read_text())] == []

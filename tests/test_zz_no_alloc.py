@@ -95,6 +95,38 @@ def test_static_mixed_then_smaller(hip_device):
     _pair(big, small, torch.bfloat16, hip_device, expect_kind="prefill")
 
 
+def test_static_entry_captured_in_a_graph(hip_device):
+    """kvh_paged_attention_static captured in a HIP graph and replayed over fresh queries and
+    edited sequence lengths: every replay equals the workspace call on the same inputs bit for
+    bit, with eager work and synchronisations between replays. One eager call on the device
+    comes first (it resolves the scratch's device address and the occupancy the launches are
+    sized by, neither of which is a stream operation to record)."""
+    w = workloads.custom("graph_mixed", [1, 1, 80, 5, 1], [300, 2000, 500, 900, 17], 32, 8, 128, 16, seed=31)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=31)
+    HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping)
+    out = torch.full_like(b.q, float("nan"))
+    assert _static_call(b, out) == 0
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = _static_call(b, out)
+    assert st == 0, _lib.strerror(st)
+    gen = torch.Generator(device=hip_device).manual_seed(5)
+    base_len = b.meta.seq_lens.clone()
+    for rep in (1, 2, 3, 0):  # the last replay with the workload's own lengths, for the oracle
+        print(f"no-alloc graph replay {rep}", flush=True)
+        b.q.copy_(torch.randn(b.q.shape, generator=gen, device=hip_device).to(b.q.dtype))
+        b.meta.seq_lens.copy_(base_len)
+        b.meta.seq_lens[1] -= 400 * rep  # the long decode sequence sees fewer keys
+        out.fill_(float("nan"))
+        graph.replay()
+        ref = HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale)
+        torch.cuda.synchronize()
+        assert torch.equal(ref.view(torch.int16), out.view(torch.int16)), f"replay {rep}"
+    err = pc.max_err_vs_oracle(b, out, list(range(len(w.query_lens))), rows_per_seq=16)
+    assert err <= pc.TOL_16BIT, err
+
+
 def test_static_rejects_oversized_launch(hip_device):
     """A launch whose workspace exceeds the static scratch (256 MiB) is rejected with
     KVH_E_SCRATCH before any GPU work: a mixed step of 2000 decode sequences and 4 prefills."""
