@@ -4,6 +4,7 @@
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-secondary]
     python bench.py --only N [--fp8]      # one BASELINE config (E4M3 KV caches with --fp8)
     python bench.py --sweep               # the reference's decode-kernel grid (bench/bench_kernel.py)
+    python bench.py --probes              # attainable HBM read / copy and bf16 MFMA rates of this GPU
 
 Headline workload: BASELINE config 2 (Llama-3.1-8B decode layer: 64 sequences, 32 q / 8 kv
 heads, head_dim 128, block 16, contexts U[1024, 8192], bf16), the config the metric is
@@ -87,6 +88,23 @@ def write_bytes(w, elem: int) -> int:
     return 2 * 2 * w.num_tokens * w.num_kv_heads * w.head_dim * elem
 
 
+def to_fp8_caches(b) -> dict:
+    """Replace the batch's bf16 caches by E4M3 caches of the same values (scales 1 / 0.5),
+    quantized on the device in slices; returns the scale arguments of the fp8 calls."""
+    import torch
+
+    kw = {"k_scale": 1.0, "v_scale": 0.5}
+    for name in ("k_cache", "v_cache"):
+        c, s = getattr(b, name), kw["k_scale" if name == "k_cache" else "v_scale"]
+        c8 = torch.empty(c.shape, dtype=torch.float8_e4m3fn, device=c.device)
+        step_blocks = max(1, (1 << 26) // c[0].numel())
+        for b0 in range(0, c.shape[0], step_blocks):
+            c8[b0 : b0 + step_blocks] = (c[b0 : b0 + step_blocks].float() / s).clamp(-448, 448).to(c8.dtype)
+        setattr(b, name, c8)
+        del c
+    return kw
+
+
 def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0, fp8: bool = False) -> dict:
     """One BASELINE config, bf16 q/out; fp8: the caches in E4M3 (scales 1 / 0.5, quantized
     from the same N(0, 1) values), K/V bytes counted at one byte per element."""
@@ -98,17 +116,7 @@ def measure(idx: int, steps: int, warmup: int, prof_iters: int, seed: int = 0, f
     b = workloads.materialize(w, torch.bfloat16, "cuda:0", seed=seed)
     elem = 2
     kv_elem = 1 if fp8 else 2
-    kw = {}
-    if fp8:
-        kw = {"k_scale": 1.0, "v_scale": 0.5}
-        for name in ("k_cache", "v_cache"):
-            c, s = getattr(b, name), kw["k_scale" if name == "k_cache" else "v_scale"]
-            c8 = torch.empty(c.shape, dtype=torch.float8_e4m3fn, device=c.device)
-            step_blocks = max(1, (1 << 26) // c[0].numel())
-            for b0 in range(0, c.shape[0], step_blocks):
-                c8[b0 : b0 + step_blocks] = (c[b0 : b0 + step_blocks].float() / s).clamp(-448, 448).to(c8.dtype)
-            setattr(b, name, c8)
-            del c
+    kw = to_fp8_caches(b) if fp8 else {}
 
     def step():
         HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping, **kw)
@@ -286,6 +294,88 @@ def measure_sweep(iters: int = 50, warmup: int = 5) -> list[dict]:
     return rows
 
 
+def measure_probes(reps: int = 10) -> dict:
+    """Attainable ceilings of this GPU from libkvhip's probes (kvh_probe): the HBM read rate of a
+    streaming kernel with the decode kernels' 16-byte loads (4 GiB, 16x the Infinity Cache), a
+    copy's read + write rate (2 GiB each way), a copy of the C3 cache write's size (8.4 MB each
+    way, after a 1 GiB read flush: the latency floor of a write that small), the dense bf16
+    MFMA rate of the prefill kernel's instruction with 1 and 2 waves per SIMD, how an MFMA wave
+    and a softmax-like VALU wave share a SIMD (each alone, then together), and what independent
+    FMAs interleaved between one wave's own MFMAs add to its time. Medians of `reps` event-timed
+    launches."""
+    import torch
+
+    from kvserve_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream().cuda_stream
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    flush = torch.zeros(FLUSH_BYTES // 4, dtype=torch.int32, device=dev)
+
+    def timed(kind, src, dst, nbytes, blocks, iters=0, cold=False):
+        for _ in range(2):
+            _lib.check(lib.kvh_probe(kind, src, dst, nbytes, blocks, iters, stream), "kvh_probe")
+        ts = []
+        for _ in range(reps):
+            if cold:
+                flush.amax()
+            start.record()
+            _lib.check(lib.kvh_probe(kind, src, dst, nbytes, blocks, iters, stream), "kvh_probe")
+            end.record()
+            end.synchronize()
+            ts.append(start.elapsed_time(end))
+        return statistics.median(ts)
+
+    res = {"cus": cus}
+    big = torch.randint(0, 1 << 30, ((4 << 30) // 4,), dtype=torch.int32, device=dev)
+    for wgs_per_cu in (4, 8):
+        blocks = cus * wgs_per_cu
+        sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+        ms = timed(0, big.data_ptr(), sink.data_ptr(), 4 << 30, blocks)
+        res[f"stream_read_gbs_{wgs_per_cu}wg_per_cu"] = (4 << 30) / (ms * 1e-3) / 1e9
+    half = (2 << 30) // 4
+    src, dst = big[:half], big[half:]
+    ms = timed(1, src.data_ptr(), dst.data_ptr(), 2 << 30, cus * 8)
+    res["copy_gbs_rw"] = 2 * (2 << 30) / (ms * 1e-3) / 1e9
+    small = 2048 * 8 * 128 * 2 * 2  # the C3 cache write: 2048 tokens of K and V rows
+    # one pass per thread: 8 loads in flight, then their 8 stores
+    ms = timed(1, src.data_ptr(), dst.data_ptr(), small, small // 16 // (256 * 8), cold=True)
+    res["copy_c3_write_size_us"] = ms * 1e3
+    res["copy_c3_write_size_gbs_rw"] = 2 * small / (ms * 1e-3) / 1e9
+    del big, src, dst
+    iters = 20000
+    for waves_per_simd in (1, 2):
+        blocks = cus * waves_per_simd
+        sink = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+        ms = timed(2, None, sink.data_ptr(), 0, blocks, iters)
+        flop = blocks * 4 * 4 * iters * 16384
+        res[f"mfma_bf16_tflops_{waves_per_simd}wave_per_simd"] = flop / (ms * 1e-3) / 1e12
+    # co-issue: an MFMA wave and a VALU wave per SIMD, alone and together (VALU steps sized to
+    # about the MFMA waves' time, the prefill chunk loop's balance)
+    sink = torch.empty(cus * 512, dtype=torch.float32, device=dev)
+    it_m, it_v = 4000, 1600
+    co = {
+        "mfma_alone_ms": timed(3, None, sink.data_ptr(), 0, cus, it_m),
+        "valu_alone_ms": timed(3, None, sink.data_ptr(), it_v, cus, 0),
+        "together_ms": timed(3, None, sink.data_ptr(), it_v, cus, it_m),
+    }
+    co["together_over_longer"] = co["together_ms"] / max(co["mfma_alone_ms"], co["valu_alone_ms"])
+    res["coissue"] = co
+    # one wave interleaving its own independent FMAs between MFMAs: time over MFMAs alone
+    sink = torch.empty(cus * 2 * 256, dtype=torch.float32, device=dev)
+    alone = timed(4, None, sink.data_ptr(), 0, cus * 2, 2000)
+    res["interleave_over_mfma_alone"] = {
+        f"{nv}_fma_per_mfma": timed(4, None, sink.data_ptr(), nv, cus * 2, 2000) / alone for nv in (1, 2, 4)
+    }
+    res["hbm_peak_gbs"] = HBM_PEAK_GBS
+    res["bf16_peak_tflops"] = BF16_PEAK_TFLOPS
+    del flush
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(idx: int, budget_s: float, seed: int = 0) -> dict:
     """The reference's torch attention (restated in oracle/torch_reference.py) in fp32 on the
     host cores, one sequence at a time, on the same bf16 values."""
@@ -457,9 +547,11 @@ def measure_metadata(idx: int, steps: int = 30) -> dict:
 CALIB_ELEMS = 1 << 27  # bf16 elements of the calibration copy: 256 MiB read + 256 MiB written
 
 
-def pmc_child() -> None:
+def pmc_child(idx: int = 2, fp8: bool = False) -> None:
     """Workload of one counter pass: a plain copy of known size (torch.neg on bf16: reads and
-    writes CALIB bytes, a kernel whose name holds "neg_kernel"), then C2 write + forwards."""
+    writes CALIB bytes, a kernel whose name holds "neg_kernel"), then one BASELINE config's
+    write + three forwards (C2 unless told otherwise; E4M3 caches with fp8), each forward after a
+    1 GiB read that evicts the caches, as the HBM-cold timings are taken."""
     import torch
 
     from kvserve_amd import HipAttention, workloads
@@ -470,11 +562,14 @@ def pmc_child() -> None:
         torch.neg(x, out=y)
     torch.cuda.synchronize()
     del x, y
-    w = workloads.baseline_config(2)
+    w = workloads.baseline_config(idx)
     b = workloads.materialize(w, torch.bfloat16, "cuda:0")
-    HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping)
+    kw = to_fp8_caches(b) if fp8 else {}
+    flush = torch.zeros(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda:0")
+    HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping, **kw)
     for _ in range(3):
-        HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale)
+        flush.amax()
+        HipAttention.forward(b.q, b.k_cache, b.v_cache, b.meta, w.scale, **kw)
     torch.cuda.synchronize()
 
 
@@ -536,12 +631,14 @@ def main() -> int:
     p.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
     p.add_argument("--no-engine", action="store_true", help="skip the 1B/8B engine decode tokens/s")
     p.add_argument("--engine-only", action="store_true", help="run just the engine decode tokens/s")
+    p.add_argument("--probes", action="store_true",
+                   help="attainable HBM read / copy and bf16 MFMA rates of this GPU (libkvhip's probes)")
     p.add_argument("--sweep", action="store_true",
                    help="the reference's decode-kernel grid (32/8 heads, D 64, batch x ctx) beside its RTX 4090 GB/s")
     p.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = p.parse_args()
     if args.pmc_child:
-        pmc_child()
+        pmc_child(args.only or 2, args.fp8)
         return 0
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -566,6 +663,9 @@ def main() -> int:
         return 0
     if args.sweep:
         measure_sweep()
+        return 0
+    if args.probes:
+        print(json.dumps(measure_probes()), flush=True)
         return 0
     engine_batches = {"llama_3_2_1b": [1, 8, 32, 64, 128], "llama_3_1_8b": [1, 8, 32, 64]}
     if args.engine_only:

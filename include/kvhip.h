@@ -349,8 +349,36 @@ enum kvh_kernel_kind {
   KVH_KERNEL_REDUCE = 3,   /* log-sum-exp merge of split decode segments and prefill tiles */
   KVH_KERNEL_F32 = 4,      /* exact fp32 path */
   KVH_KERNEL_SHARE = 5,    /* shared-prefix plan of the cascade decode (long tables, decode-only batches) */
+  KVH_KERNEL_VALU16 = 6,   /* 16-bit shapes the MFMA kernels do not tile (vector-ALU kernel) */
 };
 KVH_API int kvh_last_launch_kernels(int32_t* kinds, int32_t cap);
+
+/*
+ * Measurement probes for benchmarks (no counterpart in the reference): the attainable rate of
+ * the resources the attention kernels are bound by, with the access width they use.
+ *   KVH_PROBE_STREAM_READ: reads `bytes` of src (16-byte loads, 8 in flight per thread,
+ *     grid-stride), writes one uint32 per thread of `blocks` x 256 to dst (an XOR of its reads).
+ *   KVH_PROBE_COPY: copies `bytes` of src to dst (same loads, 16-byte stores).
+ *   KVH_PROBE_MFMA: each wave of `blocks` x 4 runs 4 independent chains of `iters`
+ *     v_mfma_f32_16x16x32_bf16 (16384 FLOP each); writes one float per thread to dst.
+ *   KVH_PROBE_COISSUE: `blocks` workgroups of 512 threads (one per CU): on each SIMD one wave
+ *     runs `iters` steps of 4 MFMA chains and a second wave `bytes` steps of a softmax's vector
+ *     work (16 FMA + 16 exp2 + 8 bf16 packs + 8 dot2); either count may be 0 (those waves idle);
+ *     writes one float per thread to dst.
+ *   KVH_PROBE_INTERLEAVE: each wave of `blocks` x 4 runs `iters` steps of 8 MFMA chains, every
+ *     MFMA followed by `bytes` (0-4) independent FMAs of the same wave; one float per thread.
+ * src and dst 16-byte aligned, bytes a positive multiple of 16 (stream / copy), blocks in
+ * [1, 65535], iters > 0 (mfma, interleave). Launches on `stream` and returns at once.
+ */
+enum kvh_probe_kind {
+  KVH_PROBE_STREAM_READ = 0,
+  KVH_PROBE_COPY = 1,
+  KVH_PROBE_MFMA = 2,
+  KVH_PROBE_COISSUE = 3,
+  KVH_PROBE_INTERLEAVE = 4,
+};
+KVH_API int kvh_probe(int32_t kind, const void* src, void* dst, int64_t bytes, int32_t blocks, int32_t iters,
+                      void* stream);
 
 #ifdef __cplusplus
 }

@@ -126,6 +126,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kvh_gemv_silu_mul": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "kvh_profile_arm": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), _i32]),
     "kvh_last_launch_kernels": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int32), _i32]),
+    "kvh_probe": (ctypes.c_int, [_i32, _vp, _vp, _i64, _i32, _i32, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None

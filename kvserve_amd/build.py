@@ -37,6 +37,7 @@ SOURCES = [
     "metadata.hip",
     "paged_attention.hip",
     "paged_attention_f32.hip",
+    "probes.hip",
     "reshape_and_cache.hip",
     "rope_and_cache.hip",
 ]

@@ -677,6 +677,21 @@ int kvh_profile_arm(void* const* events, int32_t num_events) {
   return KVH_OK;
 }
 
+int kvh_probe(int32_t kind, const void* src, void* dst, int64_t bytes, int32_t blocks, int32_t iters,
+              void* stream) {
+  if (kind < KVH_PROBE_STREAM_READ || kind > KVH_PROBE_INTERLEAVE) return KVH_E_SHAPE;
+  if (blocks < 1 || blocks > 65535) return KVH_E_SHAPE;
+  const bool compute = kind >= KVH_PROBE_MFMA;
+  if (!dst || (!compute && !src)) return KVH_E_NULL;
+  if ((kind == KVH_PROBE_MFMA || kind == KVH_PROBE_INTERLEAVE) && iters <= 0) return KVH_E_SHAPE;
+  if (kind == KVH_PROBE_INTERLEAVE && (bytes < 0 || bytes > 4)) return KVH_E_SHAPE;
+  if (kind == KVH_PROBE_COISSUE && (iters < 0 || bytes < 0 || bytes > 0x7fffffff || (iters == 0 && bytes == 0)))
+    return KVH_E_SHAPE;
+  if (!compute && (bytes <= 0 || bytes % 16 != 0)) return KVH_E_SHAPE;
+  if (!aligned16(dst) || (!compute && !aligned16(src))) return KVH_E_ALIGN;
+  return launch_probe(kind, src, dst, bytes, blocks, iters, (hipStream_t)stream);
+}
+
 int kvh_last_launch_kernels(int32_t* kinds, int32_t cap) {
   const int n = g_prof.last_count;
   for (int i = 0; i < n && i < cap && i < 8; ++i) kinds[i] = g_prof.last_kinds[i];

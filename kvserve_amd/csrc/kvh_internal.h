@@ -150,6 +150,9 @@ struct MetaParams {
 
 int launch_prepare_metadata(const MetaParams& m, const int32_t* updates, int32_t num_updates, hipStream_t s);
 
+// Measurement probes (probes.hip): 0 stream read, 1 copy, 2 MFMA rate.
+int launch_probe(int kind, const void* src, void* dst, int64_t bytes, int32_t blocks, int32_t iters, hipStream_t s);
+
 // Engine-harness kernels (engine_ops.hip).
 int launch_add_rmsnorm(const void* x, int64_t x_ts, const void* d, int64_t d_ts, const void* w, void* xo,
                        int64_t xo_ts, void* h, int64_t h_ts, int64_t T, int32_t hd, float eps, int32_t dtype,

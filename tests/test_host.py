@@ -184,6 +184,28 @@ def test_workspace_follows_the_plan(lib):
     assert ws(64, 64, 30, 8, 128, 512, 16, 1, 2) == 0  # invalid shape
 
 
+@pytest.mark.parametrize(
+    ("args", "status"),
+    [
+        ((5, 0x1000, 0x2000, 1 << 20, 256, 0), E_SHAPE),  # unknown probe
+        ((4, None, 0x2000, 5, 256, 10), E_SHAPE),  # interleave: at most 4 FMAs per MFMA
+        ((4, None, 0x2000, 2, 256, 0), E_SHAPE),
+        ((3, None, 0x2000, 0, 256, 0), E_SHAPE),  # co-issue with both wave kinds idle
+        ((0, 0x1000, 0x2000, 1 << 20, 0, 0), E_SHAPE),  # no workgroups
+        ((0, 0x1000, 0x2000, 1 << 20, 70_000, 0), E_SHAPE),
+        ((0, 0x1000, None, 1 << 20, 256, 0), E_NULL),
+        ((1, None, 0x2000, 1 << 20, 256, 0), E_NULL),
+        ((0, 0x1000, 0x2000, 1000, 256, 0), E_SHAPE),  # not whole 16-byte vectors
+        ((1, 0x1008, 0x2000, 1 << 20, 256, 0), E_ALIGN),
+        ((2, None, 0x2000, 0, 256, 0), E_SHAPE),  # MFMA probe without iterations
+        ((2, None, 0x2004, 0, 256, 10), E_ALIGN),
+    ],
+)
+def test_probe_rejects_bad_arguments(lib, args, status):
+    """The measurement probes (kvh_probe) validate before any launch."""
+    assert lib.kvh_probe(*args, None) == status
+
+
 def test_get_backend_contract(monkeypatch):
     """The reference's selector (attention.py:113-124): "auto" never raises -- it falls back
     when the backend cannot run or the block size does not tile; "hip" raises RuntimeError /
