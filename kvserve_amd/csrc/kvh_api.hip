@@ -3,6 +3,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -77,12 +78,21 @@ Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t 
                                          : 0;
     // cascade over a shared prefix: share header, decode list, prefix partials, merge jobs
     pl.cascade = !pl.launch_prefill && pl.NT == 1 && B >= 2 && (int64_t)W * BS > kCascadeMinTokens;
-    pl.SG = pl.RS >= 16 ? 1 : 16 / pl.RS;
+    // A prefix group stacks the query rows of SG = XR / RS members into NX 16-row tiles
+    // (XR = 16 NX rows). Over 16-bit caches four tiles (64 rows) when the batch holds more
+    // than one tile's worth, so up to 64 / RS members read the shared K/V once; the E4M3
+    // kernel keeps one tile (its occupancy matters more than the prefix re-reads), so the
+    // partials are sized for either.
+    pl.NX = pl.cascade && (int64_t)B * pl.RS > 16 ? 4 : 1;
     const int64_t nhg = Hkv / pl.HGW;
-    pl.xslots = pl.cascade ? ((int64_t)B + pl.SG - 1) / pl.SG * nhg + kMaxDecodeWaves / pl.HGW : 0;
+    auto prefix_rows = [&](int nx) {
+      const int xr = 16 * nx, sg = cascade_group(pl.RS, nx);
+      return (((int64_t)B + sg - 1) / sg * nhg + kMaxCascadeWaves / pl.HGW) * pl.HGW * xr;
+    };
+    pl.xrows = pl.cascade ? std::max(prefix_rows(pl.NX), prefix_rows(1)) : 0;
     pl.ws_x_bytes = pl.cascade ? align_up(kShareHdr * sizeof(int64_t)) + align_up((size_t)B * sizeof(int32_t)) +
-                                     align_up((size_t)pl.xslots * pl.HGW * 16 * D * sizeof(float)) +
-                                     align_up((size_t)pl.xslots * pl.HGW * 16 * 2 * sizeof(float)) +
+                                     align_up((size_t)pl.xrows * D * sizeof(float)) +
+                                     align_up((size_t)pl.xrows * 2 * sizeof(float)) +
                                      align_up((size_t)B * nhg * kJobInts * sizeof(int32_t))
                                : 0;
     pl.ws_bytes = pl.ws_acc_bytes + pl.ws_ml_bytes + pl.ws_job_bytes + pl.ws_pacc_bytes + pl.ws_pml_bytes +
@@ -403,7 +413,11 @@ static int paged_attention_impl(const void* q, int64_t q_tok_stride, int64_t q_h
   p.NU = 0;   // set by the decode launcher from the device's occupancy
   p.NUP = 0;  // set by the prefill launcher likewise
   p.CASC = 0;  // set by the launcher when the plan has the cascade path
-  p.SG = plan.SG;
+  {
+    const int nx = kv8 ? 1 : plan.NX;  // cascade prefix group: 16-row tiles (see make_plan)
+    p.XR = 16 * nx;
+    p.SG = cascade_group(plan.RS, nx);
+  }
   p.PR = kPrefillRows;  // the prefill launcher sets its own tile rows
   if (plan.ws_bytes) {
     char* w = (char*)workspace;
@@ -428,7 +442,7 @@ static int paged_attention_impl(const void* q, int64_t q_tok_stride, int64_t q_h
       w += align_up((size_t)kMaxPrefillUnits * kPreRec * sizeof(int32_t));
     }
     if (plan.ws_x_bytes) {
-      const size_t rows = (size_t)plan.xslots * plan.HGW * 16;
+      const size_t rows = (size_t)plan.xrows;
       p.ws_share = (int64_t*)w;
       w += align_up(kShareHdr * sizeof(int64_t));
       p.ws_dec_list = (int32_t*)w;

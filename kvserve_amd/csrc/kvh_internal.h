@@ -22,6 +22,10 @@ constexpr int32_t kPrefillRows = 128;
 // when the cascade members (decode-class sequences with at least kCascadeMinChunks chunks of
 // context) share at least kCascadeMinChunks chunks of table prefix.
 constexpr int32_t kCascadeMinTokens = 8192;
+// Cascade launches use at most kMaxCascadeWaves waves (a 256-CU device holds 2048 waves of
+// the single-tile decode kernel and 1024 of the 64-row-group one): the prefix partials, up
+// to 64 rows per (slot, head), are sized for that many units, not for kMaxDecodeWaves.
+constexpr int32_t kMaxCascadeWaves = 2048;
 // Short decode: a decode-only batch of single-tile rows whose block tables hold at most
 // kShortTokens keys takes one workgroup per (sequence, kv head); its 4 waves split the chunks
 // and combine their partials in LDS, so nothing goes through the workspace and no merge
@@ -65,7 +69,8 @@ struct PAParams {
   int32_t NUP;     // work units (workgroups) of the prefill launch (16-bit cache), else 0
   int32_t PLAN;    // 1: workgroup 0 of the decode launch writes the prefill plan
   int32_t CASC;    // 1: the share kernel ran before the decode launch (cascade over a shared prefix)
-  int32_t SG;      // cascade: decode-class sequences per 16-row prefix group (16 / RS)
+  int32_t SG;      // cascade: decode-class sequences per prefix group (XR / RS)
+  int32_t XR;      // cascade: query rows per prefix group tile (16 NX: 16 or 64)
   int32_t PR;      // query rows ((token, head) pairs of one kv head) per prefill tile
   float v_scale;   // factor of every output row: the V scale of an E4M3 cache, else 1
   float* ws_acc;   // [slots, HGW, RS, D] unnormalised partial outputs of split decode segments
@@ -81,8 +86,8 @@ struct PAParams {
   // cascade, written by pa_share_kernel before the decode launch:
   int64_t* ws_share;     // [kShareHdr]: shared prefix tokens (multiple of 32, 0: none), groups, r0, sequences
   int32_t* ws_dec_list;  // [B] decode-class sequences in order
-  float* ws_xacc;        // [xslots, HGW, 16, D] partials of the prefix segments
-  float* ws_xml;         // [xslots, HGW, 16, 2]
+  float* ws_xacc;        // [xslots, HGW, XR, D] partials of the prefix segments
+  float* ws_xml;         // [xslots, HGW, XR, 2]
   int32_t* ws_xjob;      // [B * Hkv / HGW, kJobInts] merge jobs per (sequence, head group)
 };
 
@@ -93,11 +98,14 @@ struct Plan {
   bool launch_prefill;      // max_query_len > QS
   bool cascade;             // the share kernel runs and the decode kernel may take the cascade path
   bool short_decode;        // one workgroup per (sequence, kv head), no workspace, no merge
-  int32_t SG;               // cascade: sequences per prefix group
-  int64_t xslots;           // cascade: prefix partial slots
+  int32_t NX;               // cascade: 16-row tiles of a prefix group over 16-bit caches (1 or 4)
+  int64_t xrows;            // cascade: prefix partial rows (slots x HGW x tile rows)
   int64_t slots;            // partial slots: B * Hkv / HGW + kMaxDecodeWaves / HGW
   size_t ws_acc_bytes, ws_ml_bytes, ws_job_bytes, ws_pacc_bytes, ws_pml_bytes, ws_plan_bytes, ws_x_bytes, ws_bytes;
 };
+
+// Cascade: decode-class sequences per prefix group of nx 16-row tiles, RS rows each.
+inline int32_t cascade_group(int32_t RS, int32_t nx) { return RS >= 16 * nx ? 1 : 16 * nx / RS; }
 
 Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t W, int32_t BS, int32_t max_q,
                int32_t dtype);

@@ -748,8 +748,8 @@ __device__ void plan_prefill(const PAParams& p);
 // see those keys (S BS <= every member's context). The shared length L = min(S BS, smallest
 // member context) rounded down to 32-token chunks (0 when below kCascadeMinChunks chunks or
 // fewer than 2 members). The decode kernel then computes keys [0, L) once per group of SG
-// members (their query rows stacked into one 16-row tile, so the shared K/V are read
-// members / SG times instead of once per member) and each member's own keys [L, kv_total)
+// members (their query rows stacked into one tile of XR = 16 or 64 rows, so the shared K/V
+// are read members / SG times instead of once per member) and each member's own keys [L, kv_total)
 // as usual; other sequences take their whole range as usual. The merge kernel combines the
 // partials of every (sequence, head group) from one record each.
 __device__ __forceinline__ int block_min(int v, int* red) {
@@ -866,39 +866,43 @@ __global__ __launch_bounds__(kPlanThreads) void pa_share_kernel(PAParams p) {
   }
 }
 
-// Q rows of a prefix group: row n of the 16-row tile is member n / RS of group grp (its
-// decode-list index grp SG + n / RS), row n % RS of that sequence; every valid row sees all
-// L shared keys. Same k-slot order as load_q.
-template <int D, bool KV8>
-__device__ __forceinline__ void load_q_group(WaveState<D, 1>& s, const PAParams& p, int grp, int nd, int L,
+// Q rows of a prefix group (NX 16-row tiles, XR = 16 NX rows): row r = 16 t + n is member
+// r / RS of group grp (its decode-list index grp SG + r / RS), row r % RS of that sequence;
+// every valid row sees all L shared keys. Same k-slot order as load_q.
+template <int D, int NX, bool KV8>
+__device__ __forceinline__ void load_q_group(WaveState<D, NX>& s, const PAParams& p, int grp, int nd, int L,
                                              int kvh) {
   const int lane = threadIdx.x & 63;
   const int j = lane >> 4, n = lane & 15;
-  s.m[0] = -INFINITY;
-  s.l[0] = 0.f;
-  s.thr[0] = -INFINITY;
-  s.nsh[0] = 0.f;
 #pragma unroll
-  for (int i = 0; i < D / 16; ++i) s.acc[0][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int mem = n / p.RS, rr = n % p.RS;
-  const int idx = grp * p.SG + mem;
-  bool valid = mem < p.SG && idx < nd;
-  const int seq = valid ? p.ws_dec_list[idx] : 0;
-  const SeqView sv = seq_view(p, seq);
-  const int qi = rr / p.G, g = rr % p.G;
-  valid = valid && qi < sv.q_len;
-  if (valid) {
-    const uint16_t* qp = (const uint16_t*)p.q + (sv.qs + qi) * p.q_ts + (int64_t)(kvh * p.G + g) * p.q_hs;
+  for (int t = 0; t < NX; ++t) {
+    s.m[t] = -INFINITY;
+    s.l[t] = 0.f;
+    s.thr[t] = -INFINITY;
+    s.nsh[t] = 0.f;
 #pragma unroll
-    for (int c = 0; c < D / 32; ++c) {
-      const int d0 = KV8 ? 64 * (c >> 1) + 16 * j + 8 * (c & 1) : 32 * c + 8 * j;
-      s.q[0][c] = *(const u32x4*)(qp + d0);
+    for (int i = 0; i < D / 16; ++i) s.acc[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int r = 16 * t + n;
+    const int mem = r / p.RS, rr = r % p.RS;
+    const int idx = grp * p.SG + mem;
+    bool valid = mem < p.SG && idx < nd;
+    const int seq = valid ? p.ws_dec_list[idx] : 0;
+    const SeqView sv = seq_view(p, seq);
+    const int qi = rr / p.G, g = rr % p.G;
+    valid = valid && qi < sv.q_len;
+    if (valid) {
+      const uint16_t* qp = (const uint16_t*)p.q + (sv.qs + qi) * p.q_ts + (int64_t)(kvh * p.G + g) * p.q_hs;
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) {
+        const int d0 = KV8 ? 64 * (c >> 1) + 16 * j + 8 * (c & 1) : 32 * c + 8 * j;
+        s.q[t][c] = *(const u32x4*)(qp + d0);
+      }
+      s.limit[t] = L;
+    } else {
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) s.q[t][c] = u32x4{0, 0, 0, 0};
+      s.limit[t] = 0;
     }
-    s.limit[0] = L;
-  } else {
-#pragma unroll
-    for (int c = 0; c < D / 32; ++c) s.q[0][c] = u32x4{0, 0, 0, 0};
-    s.limit[0] = 0;
   }
 }
 
@@ -920,8 +924,9 @@ __device__ __forceinline__ void write_job_x(int32_t* job, int pieces, int64_t sl
 
 // Decode class: grid (NU * HGW / 4) workgroups of 4 waves; wave w of workgroup b is head
 // w % HGW of unit (4 b + w) / HGW. In mixed batches (PLAN) workgroup 0 computes the prefill
-// plan instead and the units start at workgroup 1. KV8: the cache is E4M3.
-template <class E, int D, int NT, bool KV8>
+// plan instead and the units start at workgroup 1. KV8: the cache is E4M3. NX: 16-row tiles
+// of a cascade prefix group (XR = 16 NX rows; 1 outside the cascade).
+template <class E, int D, int NT, bool KV8, int NX>
 __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
   if (p.PLAN && blockIdx.x == 0) {
     plan_prefill(p);
@@ -969,21 +974,22 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
 
   int64_t pos = a;
   if constexpr (NT == 1) {
-    // prefix segments (g, hg): the 16-row tile of group g against keys [0, L) of head group hg,
-    // read through the first sequence's table (the shared blocks); always partial
+    // prefix segments (g, hg): the XR-row tiles of group g against keys [0, L) of head group
+    // hg, read through the first sequence's table (the shared blocks); always partial
     while (pos < b && pos < P) {
       const int64_t pseg = pos / Lc;
       const int grp = (int)(pseg / NHG), hg = (int)(pseg % NHG);
       const int64_t seg_beg = pseg * Lc, seg_end = seg_beg + Lc;
       const int64_t y = b < seg_end ? b : seg_end;
       const int kvh = hg * p.HGW + hw;
-      WaveState<D, 1> st;
-      load_q_group<D, KV8>(st, p, grp, nd, L, kvh);
+      WaveState<D, NX> st;
+      load_q_group<D, NX, KV8>(st, p, grp, nd, L, kvh);
       const int64_t* btrow = p.bt + (int64_t)r0 * p.bt_rs;
-      run_chunks<E, D, 1, KV8>(st, p, btrow, kvh, (int)(pos - seg_beg) * kChunk, kChunk, (int)(y - seg_beg) * kChunk,
-                               L);  // fmt: skip
+      run_chunks<E, D, NX, KV8>(st, p, btrow, kvh, (int)(pos - seg_beg) * kChunk, kChunk, (int)(y - seg_beg) * kChunk,
+                                L);  // fmt: skip
       SeqView none{};
-      write_rows<E, D, 1>(st, p, none, 16, 0, kvh, true, p.ws_xacc, p.ws_xml, ((pseg + unit) * p.HGW + hw) * 16);
+      write_rows<E, D, NX>(st, p, none, 16 * NX, 0, kvh, true, p.ws_xacc, p.ws_xml,
+                           ((pseg + unit) * p.HGW + hw) * (16 * NX));
       pos = y;
     }
   }
@@ -1152,13 +1158,13 @@ __device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job,
   const float* ml = dec ? p.ws_ml : p.ws_pml;
   // Two piece sets: 0 = the job's own partials, row x of piece i at base(0, i) + x; 1 (cascade)
   // = the prefix segment's, row x (head x / RS, row x % RS) at row xrow + x % RS of that head's
-  // 16-row tile, base(1, i) = (xslot0 + i) HGW 16.
+  // XR-row tile, base(1, i) = (xslot0 + i) HGW XR.
   const int xpieces = casc ? job[9] : 0;
   const int64_t xslot0 = casc ? job[10] : 0;
   const int xrow = casc ? job[11] : 0;
-  auto roff = [&](int set, int x) -> int64_t { return set == 0 ? x : (x / rph) * 16 + xrow + x % rph; };
+  auto roff = [&](int set, int x) -> int64_t { return set == 0 ? x : (x / rph) * p.XR + xrow + x % rph; };
   auto base = [&](int set, int i) -> int64_t {
-    return set == 0 ? (i == 0 ? slot0 : slotb + (int64_t)stride * i) * rows : (xslot0 + i) * p.HGW * 16;
+    return set == 0 ? (i == 0 ? slot0 : slotb + (int64_t)stride * i) * rows : (xslot0 + i) * p.HGW * p.XR;
   };
   const int nsets = xpieces > 0 ? 2 : 1;
   const int t = threadIdx.x;
@@ -2173,34 +2179,43 @@ __global__ __launch_bounds__(256, 2) void pa_prefill_kernel(PAParams p) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Workgroups of 256 threads one launch of `kernel` can keep resident on the current device
-// (cached per device and kernel).
-static int resident_blocks(const void* kernel, int block_threads = 256) {
+// Workgroups of `kernel` (block_threads each) the current device holds at once, CUs x per
+// CU, cached per device and kernel; per_cu_out, if given, receives the per-CU count (waves
+// per SIMD for 4-wave workgroups).
+static int resident_blocks(const void* kernel, int block_threads = 256, int* per_cu_out = nullptr) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    if (per_cu_out) *per_cu_out = 1;
+    return 256;
+  }
   struct Entry {
     int dev;
     const void* kernel;
-    int blocks;
+    int blocks, per_cu;
   };
-  static thread_local Entry cache[8];
+  static thread_local Entry cache[16];
   static thread_local int cache_n = 0;
   for (int i = 0; i < cache_n; ++i)
-    if (cache[i].dev == dev && cache[i].kernel == kernel) return cache[i].blocks;
+    if (cache[i].dev == dev && cache[i].kernel == kernel) {
+      if (per_cu_out) *per_cu_out = cache[i].per_cu;
+      return cache[i].blocks;
+    }
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block_threads, 0) != hipSuccess || per_cu <= 0)
     per_cu = 1;
   const int blocks = cus * per_cu;
-  if (cache_n < 8) cache[cache_n++] = Entry{dev, kernel, blocks};
+  if (cache_n < 16) cache[cache_n++] = Entry{dev, kernel, blocks, per_cu};
+  if (per_cu_out) *per_cu_out = per_cu;
   return blocks;
 }
 
-template <class E, int D, int NT, bool KV8>
+template <class E, int D, int NT, bool KV8, int NX = 1>
 static int launch_decode_nt(PAParams& p, hipStream_t s) {
-  const void* k = (const void*)&pa_decode_kernel<E, D, NT, KV8>;
+  const void* k = (const void*)&pa_decode_kernel<E, D, NT, KV8, NX>;
   const int plan_wgs = p.PLAN ? 1 : 0;  // workgroup 0 plans the prefill launch
-  int waves = (resident_blocks(k) - plan_wgs) * kWavesPerWG;
+  int per_cu = 1;
+  int waves = (resident_blocks(k, 256, &per_cu) - plan_wgs) * kWavesPerWG;
   if (waves > kMaxDecodeWaves) waves = kMaxDecodeWaves;
   int64_t units = waves / p.HGW;
   // 16-bit caches: half the resident waves. Each split segment leaves one fp32 partial per
@@ -2210,11 +2225,16 @@ static int launch_decode_nt(PAParams& p, hipStream_t s) {
   // of the waves loses 10-20%). E4M3 caches convert every element before the MFMA and keep
   // two thirds (2 of the 3 waves per SIMD the kernel fits): with three, the last-dispatched
   // workgroups of each CU finish up to 50% later than the first (HBM-cold C2 2%, C4 4% slower
-  // than with two), while half the waves is 5% slower.
-  if (!KV8)
-    units /= 2;
-  else
-    units = units * 2 / 3;
+  // than with two), while half the waves is 5% slower. A kernel that fits one wave per SIMD
+  // (the 64-row cascade tiles, 48 or 64 verify rows) keeps them all: halving would idle
+  // half the CUs.
+  if (per_cu >= 2) {
+    if (!KV8)
+      units /= 2;
+    else
+      units = units * 2 / 3;
+  }
+  if (p.CASC && units > kMaxCascadeWaves / p.HGW) units = kMaxCascadeWaves / p.HGW;  // prefix partial slots
   // No launch takes more units than its static shape can give work (kMinUnitChunks chunks of
   // at most W BS keys per segment): a small batch dispatches a grid of its own size, and the
   // merge launch scans that many job records, not one per wave the device could hold.
@@ -2225,7 +2245,7 @@ static int launch_decode_nt(PAParams& p, hipStream_t s) {
   if (units < 1) units = 1;
   p.NU = (int32_t)units;
   const int wgs = (p.NU * p.HGW + kWavesPerWG - 1) / kWavesPerWG;
-  hipLaunchKernelGGL((pa_decode_kernel<E, D, NT, KV8>), dim3(wgs + plan_wgs), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((pa_decode_kernel<E, D, NT, KV8, NX>), dim3(wgs + plan_wgs), dim3(256), 0, s, p);
   return (int)hipGetLastError();
 }
 
@@ -2256,7 +2276,15 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipSt
     if (p.NUP < 8) p.NUP = 8;
   }
   switch (plan.NT) {
-    case 1: err = launch_decode_nt<E, D, 1, KV8>(p, s); break;
+    case 1:
+      if constexpr (!KV8) {
+        if (plan.cascade && p.XR == 64) {  // 64-row prefix groups (16-bit caches only)
+          err = launch_decode_nt<E, D, 1, KV8, 4>(p, s);
+          break;
+        }
+      }
+      err = launch_decode_nt<E, D, 1, KV8>(p, s);
+      break;
     case 2: err = launch_decode_nt<E, D, 2, KV8>(p, s); break;
     case 3: err = launch_decode_nt<E, D, 3, KV8>(p, s); break;
     case 4: err = launch_decode_nt<E, D, 4, KV8>(p, s); break;

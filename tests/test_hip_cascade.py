@@ -2,8 +2,11 @@
 start with the same physical blocks, configs[3] of BASELINE.json): the shared keys are computed
 once per group of sequences and merged with each sequence's own keys. The output must match
 the oracle as for any other batch (TorchAttention reads every sequence's table on its own,
-src/kvserve/attention.py:31-82); the cases vary the group shape (SG = 16 / (q_len G)
-sequences per 16-row tile), where the sharing stops (a diverging table, the shortest member
+src/kvserve/attention.py:31-82); the cases vary the group shape (SG = 64 / (q_len G)
+sequences per 64-row group over 16-bit caches when the batch has more than 16 rows, else
+16 / (q_len G) per 16-row group, and always 16-row groups over E4M3 caches: one group of 16
+in g4_b16, two in g4_b23_ragged, 16-row groups in g1_b5_sg16 and d64_bs32_b2, 4 and 5
+members of 16 and 12 rows in g8_q2_sg1 and g4_q3_rs12), where the sharing stops (a diverging table, the shortest member
 context), members that do not join (padding rows, short contexts), E4M3 caches and graph
 replays whose metadata switches the cascade on and off.
 """

@@ -180,6 +180,25 @@ def test_workspace_follows_the_plan(lib):
     assert ws(160, 32, 32, 8, 128, 257, 16, 5, 2) == want(32, 8, 4, 5, 128)  # C5: verify rows
     assert ws(2048, 516, 32, 8, 128, 280, 16, 384, 2) == want(516, 8, 4, 4, 128, prefill=True)  # C3
     assert ws(8, 8, 16, 2, 64, 128, 16, 1, 2) == want(8, 2, 8, 1, 64, hgw=2)  # two kv heads
+
+    def cascade(B, Hkv, RS, D, hgw=8):
+        # share header, decode list, prefix partials for 64-row groups (16-bit caches, when
+        # the batch has more than 16 rows) or 16-row groups (E4M3 caches), whichever is
+        # larger: (groups x head groups + 2048 / hgw unit slots) x hgw x group rows, and one
+        # merge record per (sequence, head group)
+        up = lambda x: -(-x // 256) * 256  # noqa: E731
+        nhg = Hkv // hgw
+
+        def rows(nx):
+            sg = 1 if RS >= 16 * nx else 16 * nx // RS
+            return (-(-B // sg) * nhg + 2048 // hgw) * hgw * 16 * nx
+
+        xr = max(rows(4 if B * RS > 16 else 1), rows(1))
+        return up(8 * 8) + up(B * 4) + up(xr * D * 4) + up(xr * 2 * 4) + up(B * nhg * 16 * 4)
+
+    # C4: tables over 8192 keys plan the cascade over a shared prefix
+    assert ws(16, 16, 32, 8, 128, 2000, 16, 1, 2) == want(16, 8, 4, 1, 128) + cascade(16, 8, 4, 128)
+    assert ws(5, 5, 16, 16, 128, 600, 16, 1, 2) == want(5, 16, 1, 1, 128) + cascade(5, 16, 1, 128)
     assert ws(64, 64, 32, 8, 128, 512, 16, 1, 0) == 0  # fp32 path: no split
     assert ws(64, 64, 30, 8, 128, 512, 16, 1, 2) == 0  # invalid shape
 
