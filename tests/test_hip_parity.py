@@ -7,6 +7,8 @@ Tolerance: max-abs <= 2e-2 for bf16/fp16 storage against the oracle on the same 
 inputs (stricter than the reference's atol=rtol=2e-2), 1e-4 for the fp32 path.
 """
 
+import random
+
 import numpy as np
 import pytest
 import torch
@@ -33,6 +35,24 @@ def test_reference_cases(hip_device, case, heads, dtype):
     ref = pc.torch_oracle_full(b)
     err = (out.float().cpu() - ref).abs().max().item()
     assert err <= pc.TOL_16BIT, f"{case} {heads} {dtype}: max abs err {err}"
+
+
+@pytest.mark.parametrize("draft", [12, 16], ids=["48_rows", "64_rows"])
+def test_long_verify_keeps_every_wave(hip_device, draft):
+    """Speculative verify of 12 and 16 draft tokens (48 / 64 query rows per kv head: the
+    three- and four-tile decode kernels, which fit one wave per SIMD, so the launch keeps
+    every resident wave) at C5's size: 32 sequences over 2048-4096 cached tokens, against the
+    fp64 oracle on every sequence."""
+    rng = random.Random(draft)
+    ctx = [rng.randint(2048, 4096) for _ in range(32)]
+    w = workloads.custom(f"verify{draft}", [draft] * 32, ctx, 32, 8, 128, 16, seed=draft)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=draft)
+    out = pc.attend(b)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert last_launch_kernels() == ["decode", "reduce"], last_launch_kernels()
+    err = pc.max_err_vs_oracle(b, out, list(range(32)))
+    assert err <= pc.TOL_16BIT, err
 
 
 def test_head_dim_128_and_block_32(hip_device):
