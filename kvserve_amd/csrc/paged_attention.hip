@@ -42,7 +42,7 @@ namespace kvh {
 
 constexpr int kChunk = 32;  // tokens per wave iteration
 constexpr int kWavesPerWG = 4;
-// 16-row tiles per prefill wave: 3 over 16-bit caches (48 rows, 254 VGPRs, 2 workgroups per
+// 16-row tiles per prefill wave: 3 over 16-bit caches (48 rows, 238 VGPRs at D = 128, 2 workgroups per
 // CU), 2 over E4M3 caches (whose conversion registers leave no room for a third)
 template <bool KV8>
 constexpr int prefill_nt() {
