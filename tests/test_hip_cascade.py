@@ -82,6 +82,17 @@ def test_shared_prefix_matches_oracle(hip_device, name):
     print(f"{name}: {kinds} err {err:.3e}")
 
 
+@pytest.mark.parametrize("name", ["g4_b16", "g1_b5_sg16", "g4_b23_ragged"])
+def test_shared_prefix_fp16(hip_device, name):
+    """The fp16 instances of the cascade paths: one and two 64-row groups, and 16-row groups."""
+    q, c, heads, D, BS, shared, width = CASES[name]
+    w = shared_workload(q, c, heads, D, BS, shared, width, seed=9)
+    b = workloads.materialize(w, torch.float16, hip_device, seed=9)
+    out = pc.attend(b)
+    assert last_launch_kernels()[0] == "share", last_launch_kernels()
+    _check(b, out)
+
+
 def test_members_numbered_across_scan_windows(hip_device):
     """150 sequences (three 64-sequence scan windows of the decode kernel, several sequences
     per thread in the share kernel), non-members spread over all windows: each member's group
