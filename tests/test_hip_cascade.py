@@ -5,10 +5,11 @@ the oracle as for any other batch (TorchAttention reads every sequence's table o
 src/kvserve/attention.py:31-82); the cases vary the group shape (SG = 64 / (q_len G)
 sequences per 64-row group over 16-bit caches when the batch has more than 16 rows, else
 16 / (q_len G) per 16-row group, and always 16-row groups over E4M3 caches: one group of 16
-in g4_b16, two in g4_b23_ragged, 16-row groups in g1_b5_sg16 and d64_bs32_b2, 4 and 5
-members of 16 and 12 rows in g8_q2_sg1 and g4_q3_rs12), where the sharing stops (a diverging table, the shortest member
-context), members that do not join (padding rows, short contexts), E4M3 caches and graph
-replays whose metadata switches the cascade on and off.
+in g4_b16, two in g4_b23_ragged, one at D = 64 in d64_bs16_b9, 16-row groups in g1_b5_sg16
+and d64_bs32_b2, 4 and 5 members of 16 and 12 rows in g8_q2_sg1 and g4_q3_rs12), where the
+sharing stops (a diverging table, the shortest member context), members that do not join
+(padding rows, short contexts), E4M3 caches and graph replays whose metadata switches the
+cascade on and off.
 """
 
 from __future__ import annotations
@@ -64,6 +65,7 @@ CASES = {
     "g4_b16": ([1] * 16, [random.Random(1).randint(1700, 3000) for _ in range(16)], (32, 8), 128, 16, 100, 600),
     "g1_b5_sg16": ([1] * 5, [900, 1200, 2000, 1100, 5000], (16, 16), 128, 16, 50, 600),
     "d64_bs32_b2": ([1, 1], [700, 1500], (32, 8), 64, 32, 20, 300),
+    "d64_bs16_b9": ([1] * 9, [600 + 173 * i for i in range(9)], (32, 8), 64, 16, 36, 600),
     "g8_q2_sg1": ([2, 1, 2, 2, 1, 2, 1, 1, 2], [1000 + 97 * i for i in range(9)], (32, 4), 128, 16, 40, 600),
     "g4_q3_rs12": ([3, 1, 2, 3, 3, 1], [800, 1900, 600, 1500, 1000, 3000], (32, 8), 128, 16, 30, 600),
     "g4_b23_ragged": ([1] * 23, [300 + 211 * i for i in range(23)], (32, 8), 128, 16, 18, 800),
@@ -82,9 +84,10 @@ def test_shared_prefix_matches_oracle(hip_device, name):
     print(f"{name}: {kinds} err {err:.3e}")
 
 
-@pytest.mark.parametrize("name", ["g4_b16", "g1_b5_sg16", "g4_b23_ragged"])
+@pytest.mark.parametrize("name", ["g4_b16", "g1_b5_sg16", "g4_b23_ragged", "d64_bs16_b9"])
 def test_shared_prefix_fp16(hip_device, name):
-    """The fp16 instances of the cascade paths: one and two 64-row groups, and 16-row groups."""
+    """The fp16 instances of the cascade paths: one and two 64-row groups, 16-row groups, and
+    64-row groups at D = 64."""
     q, c, heads, D, BS, shared, width = CASES[name]
     w = shared_workload(q, c, heads, D, BS, shared, width, seed=9)
     b = workloads.materialize(w, torch.float16, hip_device, seed=9)
