@@ -55,6 +55,20 @@ def test_long_verify_keeps_every_wave(hip_device, draft):
     assert err <= pc.TOL_16BIT, err
 
 
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("draft", [5, 12, 16], ids=["2_tiles", "3_tiles", "4_tiles"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_verify_tiles_each_head_size(hip_device, head_dim, draft, dtype):
+    """Decode-class verify batches (draft x G = 4 rows per kv head: two, three and four 16-row
+    tiles per wave) at both MFMA head sizes and both 16-bit types, against the torch oracle."""
+    w = workloads.custom("verify_d", [draft] * 6, [40, 700, 1900, 3, 1200, 260], 32, 8, head_dim, 16, seed=draft)
+    b = workloads.materialize(w, dtype, hip_device, seed=draft)
+    out = pc.attend(b)
+    assert last_launch_kernels() == ["decode", "reduce"], last_launch_kernels()
+    err = (out.float().cpu() - pc.torch_oracle_full(b)).abs().max().item()
+    assert err <= pc.TOL_16BIT, f"D {head_dim} draft {draft} {dtype}: {err}"
+
+
 def test_head_dim_128_and_block_32(hip_device):
     w = workloads.custom("d128_bs32", [1, 9, 1], [80, 40, 1000], 32, 8, 128, 32, seed=0)
     b = workloads.materialize(w, torch.bfloat16, hip_device)
