@@ -19,7 +19,7 @@ def _bits(t: torch.Tensor) -> np.ndarray:
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=str)
-@pytest.mark.parametrize("shape", [(2048, 8, 128, 16), (37, 8, 64, 16), (5, 2, 12, 4)], ids=str)
+@pytest.mark.parametrize("shape", [(2048, 8, 128, 16), (37, 8, 64, 16), (5, 2, 12, 4), (9, 3, 5, 4)], ids=str)
 def test_write_matches_oracle(hip_device, dtype, shape):
     T, Hkv, D, BS = shape
     NB = T // BS + 11

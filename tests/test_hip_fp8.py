@@ -144,6 +144,35 @@ def test_d128_mixed_batch_uses_the_prefill_kernel(hip_device, dtype):
     assert err <= pc.TOL_16BIT, err
 
 
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("draft", [5, 12, 16], ids=["2_tiles", "3_tiles", "4_tiles"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+def test_verify_tiles_fp8(hip_device, head_dim, draft, dtype):
+    """Decode-class verify batches over E4M3 caches: two, three and four 16-row tiles per wave
+    at both MFMA head sizes and both 16-bit query types."""
+    w = workloads.custom("fp8_verify", [draft] * 6, [40, 700, 1900, 3, 1200, 260], 32, 8, head_dim, 16, seed=draft)
+    b = workloads.materialize(w, dtype, hip_device, seed=draft)
+    kc, vc = _fp8_caches(b, 0.5, 2.0)
+    out = _attend_fp8(b, kc, vc, 0.5, 2.0)
+    assert last_launch_kernels() == ["decode", "reduce"], last_launch_kernels()
+    err = (out.float().cpu() - _oracle(b, kc, vc, 0.5, 2.0)).abs().max().item()
+    assert err <= pc.TOL_16BIT, f"D {head_dim} draft {draft} {dtype}: {err}"
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+def test_short_tables_fp8(hip_device, head_dim, dtype):
+    """Decode over tables of at most 1024 keys takes the single-launch short decode over E4M3
+    caches too."""
+    w = workloads.custom("fp8_short", [1] * 7, [0, 15, 200, 511, 999, 64, 700], 32, 8, head_dim, 16, seed=6)
+    b = workloads.materialize(w, dtype, hip_device, seed=6)
+    kc, vc = _fp8_caches(b, 1.0, 0.5)
+    out = _attend_fp8(b, kc, vc, 1.0, 0.5)
+    assert last_launch_kernels() == ["decode"], last_launch_kernels()
+    err = (out.float().cpu() - _oracle(b, kc, vc, 1.0, 0.5)).abs().max().item()
+    assert err <= pc.TOL_16BIT, f"D {head_dim} {dtype}: {err}"
+
+
 def test_split_decode_segments(hip_device):
     """Long contexts next to a short one: the stream-K units split the long segments, whose
     pieces the merge kernel combines (and scales by v_scale); q_len 5 takes 2 row tiles."""

@@ -107,6 +107,17 @@ def test_fp32_path(hip_device, case):
     assert err <= pc.TOL_F32, err
 
 
+@pytest.mark.parametrize("head_dim", [160, 256])
+def test_fp32_head_dims_above_128(hip_device, head_dim):
+    """The exact-fp32 path at head sizes past 128 (four elements per lane)."""
+    w = workloads.reference_case("mixed", 32, 8, head_dim=head_dim, block_size=16, seed=5)
+    b = workloads.materialize(w, torch.float32, hip_device, seed=5)
+    out = pc.attend(b)
+    assert last_launch_kernels() == ["f32"]
+    err = pc.max_err_vs_oracle(b, out, list(range(len(w.query_lens))))
+    assert err <= pc.TOL_F32, err
+
+
 def test_fp32_any_block_size(hip_device):
     """The exact-fp32 path serves the reference's CPU-only block sizes too (e.g. 4)."""
     w = workloads.custom("bs4", [3, 1, 7], [9, 30, 0], 8, 2, 64, 4, seed=2)

@@ -1,0 +1,54 @@
+"""The measurement probes behind `bench.py --probes` (kvh_probe) compute what they claim, so
+the ceilings they report are measurements of real work (GPU): the stream read folds every
+dword of its buffer into its sink (the XOR of the sink equals the XOR of the buffer), the copy
+copies exactly, and the MFMA, co-issue and interleave probes run to finite sums. Small sizes;
+no timing."""
+
+import numpy as np
+import pytest
+import torch
+
+from kvserve_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def _probe(lib, kind, src, dst, nbytes, blocks, iters):
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.kvh_probe(kind, src, dst, nbytes, blocks, iters, stream), "kvh_probe")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("nbytes,blocks", [(1 << 20, 4), (3 * (1 << 20) + 4096, 7)])
+def test_stream_read_reads_every_dword(hip_device, nbytes, blocks):
+    """Buffers the grid does not divide evenly (the tail loop) included."""
+    lib = _lib.load()
+    g = torch.Generator(device=hip_device).manual_seed(nbytes)
+    src = torch.randint(-(1 << 31), (1 << 31) - 1, (nbytes // 4,), generator=g, dtype=torch.int32, device=hip_device)
+    sink = torch.zeros(blocks * 256, dtype=torch.int32, device=hip_device)
+    _probe(lib, 0, src.data_ptr(), sink.data_ptr(), nbytes, blocks, 0)
+    want = np.bitwise_xor.reduce(src.cpu().numpy().view(np.uint32))
+    got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
+    assert got == want
+
+
+def test_copy_is_exact(hip_device):
+    lib = _lib.load()
+    n = (5 << 20) + 1024
+    src = torch.randint(-(1 << 31), (1 << 31) - 1, (n // 4,), dtype=torch.int32, device=hip_device)
+    dst = torch.zeros_like(src)
+    _probe(lib, 1, src.data_ptr(), dst.data_ptr(), n, 9, 0)
+    assert torch.equal(src, dst)
+
+
+@pytest.mark.parametrize(
+    ("kind", "nbytes", "iters", "threads"),
+    [(2, 0, 100, 256), (3, 50, 100, 512), (3, 0, 100, 512), (3, 50, 0, 512), (4, 0, 50, 256), (4, 4, 50, 256)],
+    ids=["mfma", "coissue_both", "coissue_mfma", "coissue_valu", "interleave_0", "interleave_4"],
+)
+def test_compute_probes_run_to_finite_sums(hip_device, kind, nbytes, iters, threads):
+    lib = _lib.load()
+    blocks = 8
+    sink = torch.full((blocks * threads,), float("nan"), dtype=torch.float32, device=hip_device)
+    _probe(lib, kind, None, sink.data_ptr(), nbytes, blocks, iters)
+    assert torch.isfinite(sink).all()
