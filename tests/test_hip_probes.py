@@ -43,8 +43,9 @@ def test_copy_is_exact(hip_device):
 
 @pytest.mark.parametrize(
     ("kind", "nbytes", "iters", "threads"),
-    [(2, 0, 100, 256), (3, 50, 100, 512), (3, 0, 100, 512), (3, 50, 0, 512), (4, 0, 50, 256), (4, 4, 50, 256)],
-    ids=["mfma", "coissue_both", "coissue_mfma", "coissue_valu", "interleave_0", "interleave_4"],
+    [(2, 0, 100, 256), (3, 50, 100, 512), (3, 0, 100, 512), (3, 50, 0, 512)]
+    + [(4, nv, 50, 256) for nv in range(5)],
+    ids=["mfma", "coissue_both", "coissue_mfma", "coissue_valu"] + [f"interleave_{nv}" for nv in range(5)],
 )
 def test_compute_probes_run_to_finite_sums(hip_device, kind, nbytes, iters, threads):
     lib = _lib.load()
