@@ -335,6 +335,9 @@ def measure_probes(reps: int = 10) -> dict:
         sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
         ms = timed(0, big.data_ptr(), sink.data_ptr(), 4 << 30, blocks)
         res[f"stream_read_gbs_{wgs_per_cu}wg_per_cu"] = (4 << 30) / (ms * 1e-3) / 1e9
+        # the same with non-temporal loads (the decode kernels' K/V loads)
+        ms = timed(5, big.data_ptr(), sink.data_ptr(), 4 << 30, blocks)
+        res[f"stream_read_nt_gbs_{wgs_per_cu}wg_per_cu"] = (4 << 30) / (ms * 1e-3) / 1e9
     half = (2 << 30) // 4
     src, dst = big[:half], big[half:]
     ms = timed(1, src.data_ptr(), dst.data_ptr(), 2 << 30, cus * 8)

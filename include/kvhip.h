@@ -367,6 +367,8 @@ KVH_API int kvh_last_launch_kernels(int32_t* kinds, int32_t cap);
  *     writes one float per thread to dst.
  *   KVH_PROBE_INTERLEAVE: each wave of `blocks` x 4 runs `iters` steps of 8 MFMA chains, every
  *     MFMA followed by `bytes` (0-4) independent FMAs of the same wave; one float per thread.
+ *   KVH_PROBE_STREAM_READ_NT: KVH_PROBE_STREAM_READ with non-temporal loads (the decode
+ *     kernels' K/V loads).
  * src and dst 16-byte aligned, bytes a positive multiple of 16 (stream / copy), blocks in
  * [1, 65535], iters > 0 (mfma, interleave). Launches on `stream` and returns at once.
  */
@@ -376,6 +378,7 @@ enum kvh_probe_kind {
   KVH_PROBE_MFMA = 2,
   KVH_PROBE_COISSUE = 3,
   KVH_PROBE_INTERLEAVE = 4,
+  KVH_PROBE_STREAM_READ_NT = 5,
 };
 KVH_API int kvh_probe(int32_t kind, const void* src, void* dst, int64_t bytes, int32_t blocks, int32_t iters,
                       void* stream);

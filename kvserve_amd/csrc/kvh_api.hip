@@ -693,9 +693,9 @@ int kvh_profile_arm(void* const* events, int32_t num_events) {
 
 int kvh_probe(int32_t kind, const void* src, void* dst, int64_t bytes, int32_t blocks, int32_t iters,
               void* stream) {
-  if (kind < KVH_PROBE_STREAM_READ || kind > KVH_PROBE_INTERLEAVE) return KVH_E_SHAPE;
+  if (kind < KVH_PROBE_STREAM_READ || kind > KVH_PROBE_STREAM_READ_NT) return KVH_E_SHAPE;
   if (blocks < 1 || blocks > 65535) return KVH_E_SHAPE;
-  const bool compute = kind >= KVH_PROBE_MFMA;
+  const bool compute = kind >= KVH_PROBE_MFMA && kind <= KVH_PROBE_INTERLEAVE;
   if (!dst || (!compute && !src)) return KVH_E_NULL;
   if ((kind == KVH_PROBE_MFMA || kind == KVH_PROBE_INTERLEAVE) && iters <= 0) return KVH_E_SHAPE;
   if (kind == KVH_PROBE_INTERLEAVE && (bytes < 0 || bytes > 4)) return KVH_E_SHAPE;

@@ -154,10 +154,23 @@ __device__ __forceinline__ LaneOffsets lane_offsets(const PAParams& p) {
   return o;
 }
 
+// K/V of the decode kernels are read once per launch: non-temporal loads (NTL; the `nt` cache
+// policy), which the caches do not keep. Against ordinary loads, HBM-cold: C2 decode
+// 222.7 -> 200.0 us, C5 88.5 -> 80.4 us, C3's decode part 782 -> 722 us, C2 over E4M3
+// 128.7 -> 122.8 us. The short decode kernel keeps ordinary loads: on C1's 5 MB batch the
+// non-temporal ones took 11.9 us against 10.8.
+template <class T, bool NTL>
+__device__ __forceinline__ T stream_load(const void* p) {
+  if constexpr (NTL)
+    return __builtin_nontemporal_load((const T*)p);
+  else
+    return *(const T*)p;
+}
+
 // Loads are unconditional so the chunk loop stays straight-line (no waits merged at
 // branch joins): an absent tile (blk < 0) reads block 0, which the API guarantees exists,
 // and is masked out of the scores and zeroed out of V like any invalid key.
-template <int D>
+template <int D, bool NTL>
 __device__ __forceinline__ void load_k(KRegs<D>& r, const PAParams& p, const ChunkRef& c, int kvh, uint32_t k_lane) {
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -165,11 +178,11 @@ __device__ __forceinline__ void load_k(KRegs<D>& r, const PAParams& p, const Chu
     const int slot0 = (c.tok0 + 16 * t) % p.BS;
     const char* page = (const char*)p.kc + (blk * p.k_sb + (int64_t)kvh * p.k_sh + (int64_t)slot0 * p.k_ss) * 2;
 #pragma unroll
-    for (int cc = 0; cc < D / 32; ++cc) r.k[t][cc] = *(const u32x4*)(page + k_lane + 64 * cc);
+    for (int cc = 0; cc < D / 32; ++cc) r.k[t][cc] = stream_load<u32x4, NTL>(page + k_lane + 64 * cc);
   }
 }
 
-template <int D>
+template <int D, bool NTL>
 __device__ __forceinline__ void load_v(VRegs<D>& r, const PAParams& p, const ChunkRef& c, int kvh, uint32_t v_lane) {
   constexpr int VD = D / 32;
 #pragma unroll
@@ -181,13 +194,13 @@ __device__ __forceinline__ void load_v(VRegs<D>& r, const PAParams& p, const Chu
     for (int e = 0; e < 4; ++e) {
       const char* src = page + (int64_t)e * p.v_ss * 2 + v_lane;
       if constexpr (VD == 4) {
-        const u32x4 x = *(const u32x4*)src;
+        const u32x4 x = stream_load<u32x4, NTL>(src);
         r.v[4 * t + e][0] = x[0];
         r.v[4 * t + e][1] = x[1];
         r.v[4 * t + e][2] = x[2];
         r.v[4 * t + e][3] = x[3];
       } else {
-        const u32x2 x = *(const u32x2*)src;
+        const u32x2 x = stream_load<u32x2, NTL>(src);
         r.v[4 * t + e][0] = x[0];
         r.v[4 * t + e][1] = x[1];
       }
@@ -195,7 +208,7 @@ __device__ __forceinline__ void load_v(VRegs<D>& r, const PAParams& p, const Chu
   }
 }
 
-template <int D>
+template <int D, bool NTL>
 __device__ __forceinline__ void load_k(KRegs8<D>& r, const PAParams& p, const ChunkRef& c, int kvh, uint32_t k_lane) {
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -203,11 +216,11 @@ __device__ __forceinline__ void load_k(KRegs8<D>& r, const PAParams& p, const Ch
     const int slot0 = (c.tok0 + 16 * t) % p.BS;
     const char* page = (const char*)p.kc + blk * p.k_sb + (int64_t)kvh * p.k_sh + (int64_t)slot0 * p.k_ss;
 #pragma unroll
-    for (int cc = 0; cc < D / 64; ++cc) r.k[t][cc] = *(const u32x4*)(page + k_lane + 64 * cc);
+    for (int cc = 0; cc < D / 64; ++cc) r.k[t][cc] = stream_load<u32x4, NTL>(page + k_lane + 64 * cc);
   }
 }
 
-template <int D>
+template <int D, bool NTL>
 __device__ __forceinline__ void load_v(VRegs8<D>& r, const PAParams& p, const ChunkRef& c, int kvh, uint32_t v_lane) {
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -218,11 +231,11 @@ __device__ __forceinline__ void load_v(VRegs8<D>& r, const PAParams& p, const Ch
     for (int e = 0; e < 4; ++e) {
       const char* src = page + (int64_t)e * p.v_ss + v_lane;
       if constexpr (D == 128) {
-        const u32x2 x = *(const u32x2*)src;
+        const u32x2 x = stream_load<u32x2, NTL>(src);
         r.v[4 * t + e][0] = x[0];
         r.v[4 * t + e][1] = x[1];
       } else {
-        r.v[4 * t + e][0] = *(const uint32_t*)src;
+        r.v[4 * t + e][0] = stream_load<uint32_t, NTL>(src);
       }
     }
   }
@@ -518,7 +531,7 @@ __device__ __forceinline__ void chunk_pv(WaveState<D, NT>& s, VRegs8<D>& vr, con
 // The body is straight-line (masks always applied, loads unconditional) and the loads are
 // pinned in the order K(c+1), V(c+1) with scheduling barriers, so each s_waitcnt waits for
 // exactly the operand it guards while the other half of the next chunk stays in flight.
-template <class E, int D, int NT, bool KV8 = false>
+template <class E, int D, int NT, bool KV8 = false, bool NTL = true>
 __device__ __forceinline__ void run_chunks(WaveState<D, NT>& s, const PAParams& p, const int64_t* btrow, int kvh,
                                            int tok_begin, int stride, int tok_hi, int data_end) {
   if (tok_begin >= tok_hi) return;
@@ -529,9 +542,9 @@ __device__ __forceinline__ void run_chunks(WaveState<D, NT>& s, const PAParams& 
   ChunkRef c = chunk_ref(pw, p, btrow, tok_begin, tok_hi, page_end);
   std::conditional_t<KV8, KRegs8<D>, KRegs<D>> kr;
   std::conditional_t<KV8, VRegs8<D>, VRegs<D>> vr;
-  load_k<D>(kr, p, c, kvh, lo.k);
+  load_k<D, NTL>(kr, p, c, kvh, lo.k);
   __builtin_amdgcn_sched_barrier(0);
-  load_v<D>(vr, p, c, kvh, lo.v);
+  load_v<D, NTL>(vr, p, c, kvh, lo.v);
   __builtin_amdgcn_sched_barrier(0);
   // Every iteration has a next chunk, so its loads are unconditional; the last chunk is
   // peeled off below the loop.
@@ -540,11 +553,11 @@ __device__ __forceinline__ void run_chunks(WaveState<D, NT>& s, const PAParams& 
     u32x4 pt[NT];
     chunk_scores<E, D, NT, true>(s, kr, p, c, pt);
     __builtin_amdgcn_sched_barrier(0);
-    load_k<D>(kr, p, cn, kvh, lo.k);
+    load_k<D, NTL>(kr, p, cn, kvh, lo.k);
     __builtin_amdgcn_sched_barrier(0);
     chunk_pv<E, D, NT, true>(s, vr, c, data_end, pt);
     __builtin_amdgcn_sched_barrier(0);
-    load_v<D>(vr, p, cn, kvh, lo.v);
+    load_v<D, NTL>(vr, p, cn, kvh, lo.v);
     __builtin_amdgcn_sched_barrier(0);
     c = cn;
   }
@@ -1077,7 +1090,7 @@ __global__ __launch_bounds__(256) void pa_decode_short_kernel(PAParams p) {
   WaveState<D, 1> st;
   load_q<D, 1, KV8>(st, p, sv.qs, R, 0, kvh, sv.ctx, sv.kv_total);
   const int64_t* btrow = p.bt + (int64_t)seq * p.bt_rs;
-  run_chunks<E, D, 1, KV8>(st, p, btrow, kvh, w * kChunk, kWavesPerWG * kChunk, sv.kv_total, sv.kv_total);
+  run_chunks<E, D, 1, KV8, false>(st, p, btrow, kvh, w * kChunk, kWavesPerWG * kChunk, sv.kv_total, sv.kv_total);
   if (w > 0) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) x_acc[w - 1][i][lane] = st.acc[0][i];

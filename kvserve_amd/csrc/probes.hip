@@ -3,7 +3,8 @@
 // access widths the kernels use, so a kernel's rate can be read against an attainable ceiling
 // as well as against the published peak.
 //
-//  * stream read: 16-byte loads per lane, kProbeUnroll loads in flight per thread, grid-stride
+//  * stream read: 16-byte loads per lane (ordinary, or non-temporal as the decode kernels'
+//    K/V loads), kProbeUnroll loads in flight per thread, grid-stride
 //    over a buffer much larger than the Infinity Cache, an XOR of everything read kept per thread
 //    (so no load is dead) and one dword written per thread: the HBM read rate a streaming kernel
 //    can reach (the decode kernels' bound).
@@ -22,6 +23,16 @@ namespace kvh {
 constexpr int kProbeUnroll = 8;
 constexpr int kProbeChains = 4;
 
+// NT: non-temporal loads (the decode kernels' K/V loads), else ordinary ones
+template <bool NT>
+__device__ __forceinline__ u32x4 probe_load(const u32x4* p) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load(p);
+  else
+    return *p;
+}
+
+template <bool NT>
 __global__ __launch_bounds__(256) void probe_stream_read_kernel(const u32x4* src, int64_t n, uint32_t* sink) {
   const int64_t stride = (int64_t)gridDim.x * 256;
   int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -29,11 +40,11 @@ __global__ __launch_bounds__(256) void probe_stream_read_kernel(const u32x4* src
   for (; i + (kProbeUnroll - 1) * stride < n; i += kProbeUnroll * stride) {
     u32x4 v[kProbeUnroll];
 #pragma unroll
-    for (int u = 0; u < kProbeUnroll; ++u) v[u] = src[i + u * stride];
+    for (int u = 0; u < kProbeUnroll; ++u) v[u] = probe_load<NT>(src + i + u * stride);
 #pragma unroll
     for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u];
   }
-  for (; i < n; i += stride) acc ^= src[i];
+  for (; i < n; i += stride) acc ^= probe_load<NT>(src + i);
   sink[(int64_t)blockIdx.x * 256 + threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 }
 
@@ -168,7 +179,11 @@ int launch_probe(int kind, const void* src, void* dst, int64_t bytes, int32_t bl
   }
   const int64_t n = bytes / 16;
   if (kind == 0)
-    hipLaunchKernelGGL(probe_stream_read_kernel, dim3(blocks), dim3(256), 0, s, (const u32x4*)src, n, (uint32_t*)dst);
+    hipLaunchKernelGGL(probe_stream_read_kernel<false>, dim3(blocks), dim3(256), 0, s, (const u32x4*)src, n,
+                       (uint32_t*)dst);
+  else if (kind == 5)
+    hipLaunchKernelGGL(probe_stream_read_kernel<true>, dim3(blocks), dim3(256), 0, s, (const u32x4*)src, n,
+                       (uint32_t*)dst);
   else if (kind == 1)
     hipLaunchKernelGGL(probe_copy_kernel, dim3(blocks), dim3(256), 0, s, (const u32x4*)src, (u32x4*)dst, n);
   else

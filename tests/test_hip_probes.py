@@ -19,14 +19,16 @@ def _probe(lib, kind, src, dst, nbytes, blocks, iters):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("kind", [0, 5], ids=["ordinary", "non_temporal"])
 @pytest.mark.parametrize("nbytes,blocks", [(1 << 20, 4), (3 * (1 << 20) + 4096, 7)])
-def test_stream_read_reads_every_dword(hip_device, nbytes, blocks):
-    """Buffers the grid does not divide evenly (the tail loop) included."""
+def test_stream_read_reads_every_dword(hip_device, kind, nbytes, blocks):
+    """Buffers the grid does not divide evenly (the tail loop) included; ordinary and
+    non-temporal loads."""
     lib = _lib.load()
     g = torch.Generator(device=hip_device).manual_seed(nbytes)
     src = torch.randint(-(1 << 31), (1 << 31) - 1, (nbytes // 4,), generator=g, dtype=torch.int32, device=hip_device)
     sink = torch.zeros(blocks * 256, dtype=torch.int32, device=hip_device)
-    _probe(lib, 0, src.data_ptr(), sink.data_ptr(), nbytes, blocks, 0)
+    _probe(lib, kind, src.data_ptr(), sink.data_ptr(), nbytes, blocks, 0)
     want = np.bitwise_xor.reduce(src.cpu().numpy().view(np.uint32))
     got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
     assert got == want
