@@ -296,8 +296,9 @@ def measure_sweep(iters: int = 50, warmup: int = 5) -> list[dict]:
 
 def measure_probes(reps: int = 10) -> dict:
     """Attainable ceilings of this GPU from libkvhip's probes (kvh_probe): the HBM read rate of a
-    streaming kernel with the decode kernels' 16-byte loads (4 GiB, 16x the Infinity Cache), a
-    copy's read + write rate (2 GiB each way), a copy of the C3 cache write's size (8.4 MB each
+    streaming kernel with the decode kernels' 16-byte loads (4 GiB, 16x the Infinity Cache;
+    ordinary and non-temporal loads), of a gather of scattered 4 KB pages (the decode kernels'
+    access pattern, non-temporal), a copy's read + write rate (2 GiB each way), a copy of the C3 cache write's size (8.4 MB each
     way, after a 1 GiB read flush: the latency floor of a write that small), the dense bf16
     MFMA rate of the prefill kernel's instruction with 1 and 2 waves per SIMD, how an MFMA wave
     and a softmax-like VALU wave share a SIMD (each alone, then together), and what independent
@@ -330,7 +331,7 @@ def measure_probes(reps: int = 10) -> dict:
 
     res = {"cus": cus}
     big = torch.randint(0, 1 << 30, ((4 << 30) // 4,), dtype=torch.int32, device=dev)
-    for wgs_per_cu in (4, 8):
+    for wgs_per_cu in (2, 4, 8):
         blocks = cus * wgs_per_cu
         sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
         ms = timed(0, big.data_ptr(), sink.data_ptr(), 4 << 30, blocks)
@@ -338,6 +339,8 @@ def measure_probes(reps: int = 10) -> dict:
         # the same with non-temporal loads (the decode kernels' K/V loads)
         ms = timed(5, big.data_ptr(), sink.data_ptr(), 4 << 30, blocks)
         res[f"stream_read_nt_gbs_{wgs_per_cu}wg_per_cu"] = (4 << 30) / (ms * 1e-3) / 1e9
+        ms = timed(6, big.data_ptr(), sink.data_ptr(), 4 << 30, blocks)
+        res[f"page_gather_nt_gbs_{wgs_per_cu}wg_per_cu"] = (4 << 30) / (ms * 1e-3) / 1e9
     half = (2 << 30) // 4
     src, dst = big[:half], big[half:]
     ms = timed(1, src.data_ptr(), dst.data_ptr(), 2 << 30, cus * 8)

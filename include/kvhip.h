@@ -356,9 +356,10 @@ KVH_API int kvh_last_launch_kernels(int32_t* kinds, int32_t cap);
 /*
  * Measurement probes for benchmarks (no counterpart in the reference): the attainable rate of
  * the resources the attention kernels are bound by, with the access width they use.
- *   KVH_PROBE_STREAM_READ: reads `bytes` of src (16-byte loads, 8 in flight per thread,
- *     grid-stride), writes one uint32 per thread of `blocks` x 256 to dst (an XOR of its reads).
- *   KVH_PROBE_COPY: copies `bytes` of src to dst (same loads, 16-byte stores).
+ *   KVH_PROBE_STREAM_READ: reads `bytes` of src (16-byte loads, 8 in flight per thread, each
+ *     workgroup a contiguous 1 / blocks of the buffer), writes one uint32 per thread of
+ *     `blocks` x 256 to dst (an XOR of its reads).
+ *   KVH_PROBE_COPY: copies `bytes` of src to dst (same loads and ranges, 16-byte stores).
  *   KVH_PROBE_MFMA: each wave of `blocks` x 4 runs 4 independent chains of `iters`
  *     v_mfma_f32_16x16x32_bf16 (16384 FLOP each); writes one float per thread to dst.
  *   KVH_PROBE_COISSUE: `blocks` workgroups of 512 threads (one per CU): on each SIMD one wave
@@ -369,8 +370,13 @@ KVH_API int kvh_last_launch_kernels(int32_t* kinds, int32_t cap);
  *     MFMA followed by `bytes` (0-4) independent FMAs of the same wave; one float per thread.
  *   KVH_PROBE_STREAM_READ_NT: KVH_PROBE_STREAM_READ with non-temporal loads (the decode
  *     kernels' K/V loads).
- * src and dst 16-byte aligned, bytes a positive multiple of 16 (stream / copy), blocks in
- * [1, 65535], iters > 0 (mfma, interleave). Launches on `stream` and returns at once.
+ *   KVH_PROBE_PAGE_GATHER: reads the `bytes` / 4096 pages of 4 KB of src, a power-of-two count,
+ *     in a scattered order (page (j * 0x9E3779B1) mod count at walk position j), each wave of
+ *     `blocks` x 4 its own run of positions with 4 pages in flight, non-temporal loads (the
+ *     decode kernels' access pattern); dst as for KVH_PROBE_STREAM_READ.
+ * src and dst 16-byte aligned, bytes a positive multiple of 16 (stream / copy; of 4096 with a
+ * power-of-two quotient for the page gather), blocks in [1, 65535], iters > 0 (mfma,
+ * interleave). Launches on `stream` and returns at once.
  */
 enum kvh_probe_kind {
   KVH_PROBE_STREAM_READ = 0,
@@ -379,6 +385,7 @@ enum kvh_probe_kind {
   KVH_PROBE_COISSUE = 3,
   KVH_PROBE_INTERLEAVE = 4,
   KVH_PROBE_STREAM_READ_NT = 5,
+  KVH_PROBE_PAGE_GATHER = 6,
 };
 KVH_API int kvh_probe(int32_t kind, const void* src, void* dst, int64_t bytes, int32_t blocks, int32_t iters,
                       void* stream);

@@ -693,7 +693,7 @@ int kvh_profile_arm(void* const* events, int32_t num_events) {
 
 int kvh_probe(int32_t kind, const void* src, void* dst, int64_t bytes, int32_t blocks, int32_t iters,
               void* stream) {
-  if (kind < KVH_PROBE_STREAM_READ || kind > KVH_PROBE_STREAM_READ_NT) return KVH_E_SHAPE;
+  if (kind < KVH_PROBE_STREAM_READ || kind > KVH_PROBE_PAGE_GATHER) return KVH_E_SHAPE;
   if (blocks < 1 || blocks > 65535) return KVH_E_SHAPE;
   const bool compute = kind >= KVH_PROBE_MFMA && kind <= KVH_PROBE_INTERLEAVE;
   if (!dst || (!compute && !src)) return KVH_E_NULL;
@@ -702,6 +702,8 @@ int kvh_probe(int32_t kind, const void* src, void* dst, int64_t bytes, int32_t b
   if (kind == KVH_PROBE_COISSUE && (iters < 0 || bytes < 0 || bytes > 0x7fffffff || (iters == 0 && bytes == 0)))
     return KVH_E_SHAPE;
   if (!compute && (bytes <= 0 || bytes % 16 != 0)) return KVH_E_SHAPE;
+  if (kind == KVH_PROBE_PAGE_GATHER && (bytes % 4096 != 0 || ((bytes / 4096) & (bytes / 4096 - 1)) != 0))
+    return KVH_E_SHAPE;  // a power-of-two count of 4 KB pages
   if (!aligned16(dst) || (!compute && !aligned16(src))) return KVH_E_ALIGN;
   return launch_probe(kind, src, dst, bytes, blocks, iters, (hipStream_t)stream);
 }

@@ -748,6 +748,28 @@ __device__ __forceinline__ int64_t active_units(int64_t C, int NU) {
   return want < 1 ? 1 : (want < NU ? want : NU);
 }
 
+// Stream-K split of the decode kernel's flat positions [0, C) over NUa units by cost: the first
+// P positions (cascade prefix segments) cost wp each, the others wr. Unit u takes the positions
+// whose cost start cost(x) lies in [u T / NUa, (u + 1) T / NUa), T = cost(C); wp = wr = 1 is the
+// plain split [u C / NUa, (u + 1) C / NUa).
+struct CostSplit {
+  int64_t P, C, NUa, wp, wr, T;
+  __device__ CostSplit(int64_t P_, int64_t C_, int64_t NUa_, int64_t wp_, int64_t wr_)
+      : P(P_), C(C_), NUa(NUa_), wp(wp_), wr(wr_), T(wp_ * P_ + wr_ * (C_ - P_)) {}
+  __device__ int64_t cost(int64_t x) const { return x < P ? wp * x : wp * P + wr * (x - P); }
+  // the first position whose cost start is >= c
+  __device__ int64_t first(int64_t c) const { return c <= wp * P ? (c + wp - 1) / wp : P + (c - wp * P + wr - 1) / wr; }
+  __device__ int64_t begin(int64_t u) const { return first(u * T / NUa); }
+  // the unit that takes position x: the last u with u T / NUa <= cost(x)
+  __device__ int64_t unit_of(int64_t x) const { return ((cost(x) + 1) * NUa - 1) / T; }
+};
+// Cost of a 64-row prefix position against any other position, in eighths: the 4x MFMA and
+// softmax work per chunk of the prefix tiles makes their units finish last under an even split
+// (HBM-cold C4: units of prefix positions ended at 151-162 us, the others at 141-145 us).
+// Measured on C4's decode kernel, HBM-cold: weights 8 (even) 178.7 us, 9 170.6, 10 159.4,
+// 11 154.4, 12 155.5, 13 156.1, 14 156.4, 16 158.5.
+constexpr int64_t kPrefix64Cost = 11, kChunkCost = 8;
+
 constexpr int kPlanThreads = 256;    // the decode kernel's workgroup
 constexpr int kPlanLdsSeqs = 1024;  // flat starts kept in LDS for the unit search (else global)
 __device__ void plan_prefill(const PAParams& p);
@@ -982,7 +1004,9 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
   const int64_t C = P + (int64_t)Cs * NHG;
   const int64_t NUa = active_units(C, p.NU);
   if (unit >= NUa) return;
-  const int64_t a = unit * C / NUa, b = (unit + 1) * C / NUa;
+  const bool weighted = NX > 1 && P > 0;
+  const CostSplit split(P, C, NUa, weighted ? kPrefix64Cost : 1, weighted ? kChunkCost : 1);
+  const int64_t a = split.begin(unit), b = split.begin(unit + 1);
   if (a >= b) return;
 
   int64_t pos = a;
@@ -1044,7 +1068,7 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
         // segment's own pieces in slot + i (units unit .. u1) and, for a member, the prefix
         // segment (grp, hg)'s in pseg + uf + i (units uf .. ul), rows xrow .. of its tiles
         int32_t* xj = p.ws_xjob + ((int64_t)seq * NHG + hg) * kJobInts;
-        const int64_t u1 = (seg_end * NUa - 1) / C;
+        const int64_t u1 = split.unit_of(seg_end - 1);
         if (whole) {
           xj[0] = kJobNone;
         } else if (member) {
@@ -1052,7 +1076,7 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
           const int grp = idx / p.SG, mem = idx % p.SG;
           const int64_t pseg = (int64_t)grp * NHG + hg;
           const int64_t x0 = pseg * Lc, x1 = x0 + Lc - 1;
-          const int64_t uf = ((x0 + 1) * NUa - 1) / C, ul = ((x1 + 1) * NUa - 1) / C;
+          const int64_t uf = split.unit_of(x0), ul = split.unit_of(x1);
           write_job_x(xj, (int)(u1 - unit + 1), slot, sv.qs, R, hg * p.HGW, (int)(ul - uf + 1), pseg + uf,
                       mem * p.RS);
         } else {
@@ -1061,7 +1085,7 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
       }
     } else if (job_writer && pos == seg_beg && y < seg_end) {
       // the segment starts here and continues in units unit + 1 .. u1: piece i is in slot + i
-      const int64_t u1 = (seg_end * NUa - 1) / C;
+      const int64_t u1 = split.unit_of(seg_end - 1);
       write_job(job, kJobDecode, (int)(u1 - unit + 1), slot, slot, 1, sv.qs, R, 0, hg * p.HGW);
     }
     pos = y;

@@ -1,8 +1,8 @@
 """The measurement probes behind `bench.py --probes` (kvh_probe) compute what they claim, so
-the ceilings they report are measurements of real work (GPU): the stream read folds every
-dword of its buffer into its sink (the XOR of the sink equals the XOR of the buffer), the copy
-copies exactly, and the MFMA, co-issue and interleave probes run to finite sums. Small sizes;
-no timing."""
+the ceilings they report are measurements of real work (GPU): the stream read and the page
+gather fold every dword of their buffer into their sink (the XOR of the sink equals the XOR of
+the buffer: the gather's scattered order visits every page once), the copy copies exactly, and
+the MFMA, co-issue and interleave probes run to finite sums. Small sizes; no timing."""
 
 import numpy as np
 import pytest
@@ -29,6 +29,21 @@ def test_stream_read_reads_every_dword(hip_device, kind, nbytes, blocks):
     src = torch.randint(-(1 << 31), (1 << 31) - 1, (nbytes // 4,), generator=g, dtype=torch.int32, device=hip_device)
     sink = torch.zeros(blocks * 256, dtype=torch.int32, device=hip_device)
     _probe(lib, kind, src.data_ptr(), sink.data_ptr(), nbytes, blocks, 0)
+    want = np.bitwise_xor.reduce(src.cpu().numpy().view(np.uint32))
+    got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
+    assert got == want
+
+
+@pytest.mark.parametrize("pages,blocks", [(256, 4), (64, 3), (1, 1)])
+def test_page_gather_reads_every_page(hip_device, pages, blocks):
+    """16 pages per wave (whole groups of 4 in flight), runs of 5-6 pages (the tail loop), and
+    waves with no page at all."""
+    lib = _lib.load()
+    nbytes = pages * 4096
+    g = torch.Generator(device=hip_device).manual_seed(pages)
+    src = torch.randint(-(1 << 31), (1 << 31) - 1, (nbytes // 4,), generator=g, dtype=torch.int32, device=hip_device)
+    sink = torch.zeros(blocks * 256, dtype=torch.int32, device=hip_device)
+    _probe(lib, 6, src.data_ptr(), sink.data_ptr(), nbytes, blocks, 0)
     want = np.bitwise_xor.reduce(src.cpu().numpy().view(np.uint32))
     got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
     assert got == want

@@ -206,7 +206,9 @@ def test_workspace_follows_the_plan(lib):
 @pytest.mark.parametrize(
     ("args", "status"),
     [
-        ((6, 0x1000, 0x2000, 1 << 20, 256, 0), E_SHAPE),  # unknown probe
+        ((7, 0x1000, 0x2000, 1 << 20, 256, 0), E_SHAPE),  # unknown probe
+        ((6, 0x1000, 0x2000, (1 << 20) + 16, 256, 0), E_SHAPE),  # page gather: not whole pages
+        ((6, 0x1000, 0x2000, 3 * 4096, 256, 0), E_SHAPE),  # page gather: 3 pages, not a power of two
         ((5, 0x1000, None, 1 << 20, 256, 0), E_NULL),  # non-temporal stream read: a read probe
         ((4, None, 0x2000, 5, 256, 10), E_SHAPE),  # interleave: at most 4 FMAs per MFMA
         ((4, None, 0x2000, 2, 256, 0), E_SHAPE),
