@@ -1022,8 +1022,10 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
       WaveState<D, NX> st;
       load_q_group<D, NX, KV8>(st, p, grp, nd, L, kvh);
       const int64_t* btrow = p.bt + (int64_t)r0 * p.bt_rs;
-      run_chunks<E, D, NX, KV8>(st, p, btrow, kvh, (int)(pos - seg_beg) * kChunk, kChunk, (int)(y - seg_beg) * kChunk,
-                                L);  // fmt: skip
+      // 16-row groups (NX = 1) each read the shared keys: ordinary loads, so the other groups'
+      // reads hit the Infinity Cache (non-temporal ones ran C4 over E4M3 103 -> 108 us)
+      run_chunks<E, D, NX, KV8, (NX > 1)>(st, p, btrow, kvh, (int)(pos - seg_beg) * kChunk, kChunk,
+                                          (int)(y - seg_beg) * kChunk, L);
       SeqView none{};
       write_rows<E, D, NX>(st, p, none, 16 * NX, 0, kvh, true, p.ws_xacc, p.ws_xml,
                            ((pseg + unit) * p.HGW + hw) * (16 * NX));
