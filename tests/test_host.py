@@ -2,6 +2,7 @@
 
 import ctypes
 import math
+import random
 import re
 from pathlib import Path
 
@@ -579,3 +580,51 @@ def test_prefill_priority_change_points_match_the_per_chunk_level():
                         lvl = lvl_of(i, n, rest, total)
                         nxt = drop_of(lvl, n, rest, total) if lvl > 0 else big
                     assert lvl == lvl_of(i, n, rest, total), (total, n, rest, i)
+
+
+def test_cascade_cost_split_partitions_the_positions():
+    """The decode kernel's stream-K split by cost (`CostSplit`: the first P positions cost wp,
+    the others wr) must give every position of [0, C) to exactly one unit, units in order, and
+    `unit_of` must name the unit whose range holds each position (the merge records list a
+    segment's pieces by it). Weights 1/1 must give the plain split [u C / NUa, (u + 1) C / NUa).
+    The expressions are taken from the source and checked against a walk over every position."""
+    src = (Path(__file__).resolve().parent.parent / "kvserve_amd/csrc/paged_attention.hip").read_text()
+    body = re.search(r"struct CostSplit \{(.*?)\n\};", src, re.S).group(1)
+
+    def expr(fn):  # the returned expression of a one-line member function
+        e = re.search(rf"int64_t {fn}\(int64_t \w+\) const \{{ return (.*?); \}}", body).group(1)
+        if " ? " in e:  # c ? a : b (one conditional, at the top level)
+            cond, rest = e.split(" ? ", 1)
+            a, b = rest.split(" : ", 1)
+            e = f"({a}) if ({cond}) else ({b})"
+        return e.replace("/", "//")
+
+    cost_e, first_e, begin_e, unit_e = expr("cost"), expr("first"), expr("begin"), expr("unit_of")
+    prefix_w = int(re.search(r"constexpr int64_t kPrefix64Cost = (\d+), kChunkCost = (\d+);", src).group(1))
+    chunk_w = int(re.search(r"constexpr int64_t kPrefix64Cost = (\d+), kChunkCost = (\d+);", src).group(2))
+
+    def split(P, C, NUa, wp, wr):
+        env = {"P": P, "C": C, "NUa": NUa, "wp": wp, "wr": wr, "T": wp * P + wr * (C - P)}
+        f = {}
+        for name, e, arg in (("cost", cost_e, "x"), ("first", first_e, "c")):
+            f[name] = eval(f"lambda {arg}: {e}", dict(env))  # noqa: S307
+        env.update(f)
+        begin = eval(f"lambda u: {begin_e}", env)  # noqa: S307 (source text of this repo)
+        unit_of = eval(f"lambda x: {unit_e}", env)  # noqa: S307
+        return begin, unit_of
+
+    rng = random.Random(5)
+    cases = [(0, 1, 1), (3, 3, 2), (375, 6375, 128)] + [
+        (rng.randint(0, c), c, rng.randint(1, 300)) for c in (rng.randint(1, 4000) for _ in range(400))
+    ]
+    for P, C, NUa in cases:
+        for wp, wr in ((1, 1), (prefix_w, chunk_w)):
+            begin, unit_of = split(P, C, NUa, wp, wr)
+            assert begin(0) == 0 and begin(NUa) == C, (P, C, NUa, wp, wr)
+            for u in range(NUa):
+                a, b = begin(u), begin(u + 1)
+                assert a <= b
+                if wp == wr == 1:
+                    assert a == u * C // NUa
+                for x in range(a, b):
+                    assert unit_of(x) == u, (P, C, NUa, wp, wr, u, x)
