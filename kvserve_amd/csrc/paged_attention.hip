@@ -748,20 +748,28 @@ __device__ __forceinline__ int64_t active_units(int64_t C, int NU) {
   return want < 1 ? 1 : (want < NU ? want : NU);
 }
 
-// Stream-K split of the decode kernel's flat positions [0, C) over NUa units by cost: the first
-// P positions (cascade prefix segments) cost wp each, the others wr. Unit u takes the positions
-// whose cost start cost(x) lies in [u T / NUa, (u + 1) T / NUa), T = cost(C); wp = wr = 1 is the
-// plain split [u C / NUa, (u + 1) C / NUa).
+// Stream-K split of the decode kernel's flat positions [0, C) over NUa units by cost, and by
+// unit capacity: the first P positions (cascade prefix segments) cost wp each, the others wr;
+// the first R1 units (those dispatched in the first round, one workgroup per CU) take K1 parts
+// of the total cost each, the later ones K2. With cum(u) the parts of units before u and
+// Q = cum(NUa), unit u takes the positions whose cost start cost(x) lies in
+// [T cum(u) / Q, T cum(u + 1) / Q), T = cost(C); wp = wr = K1 = K2 = 1 is the plain split
+// [u C / NUa, (u + 1) C / NUa).
 struct CostSplit {
-  int64_t P, C, NUa, wp, wr, T;
-  __device__ CostSplit(int64_t P_, int64_t C_, int64_t NUa_, int64_t wp_, int64_t wr_)
-      : P(P_), C(C_), NUa(NUa_), wp(wp_), wr(wr_), T(wp_ * P_ + wr_ * (C_ - P_)) {}
+  int64_t P, C, NUa, wp, wr, T, R1, K1, K2, Q;
+  __device__ CostSplit(int64_t P_, int64_t C_, int64_t NUa_, int64_t wp_, int64_t wr_, int64_t R1_, int64_t K1_,
+                       int64_t K2_)
+      : P(P_), C(C_), NUa(NUa_), wp(wp_), wr(wr_), T(wp_ * P_ + wr_ * (C_ - P_)), R1(R1_ < NUa_ ? R1_ : NUa_),
+        K1(K1_), K2(K2_), Q(K1 * R1 + K2 * (NUa - R1)) {}
   __device__ int64_t cost(int64_t x) const { return x < P ? wp * x : wp * P + wr * (x - P); }
   // the first position whose cost start is >= c
   __device__ int64_t first(int64_t c) const { return c <= wp * P ? (c + wp - 1) / wp : P + (c - wp * P + wr - 1) / wr; }
-  __device__ int64_t begin(int64_t u) const { return first(u * T / NUa); }
-  // the unit that takes position x: the last u with u T / NUa <= cost(x)
-  __device__ int64_t unit_of(int64_t x) const { return ((cost(x) + 1) * NUa - 1) / T; }
+  __device__ int64_t cum(int64_t u) const { return u <= R1 ? K1 * u : K1 * R1 + K2 * (u - R1); }
+  __device__ int64_t begin(int64_t u) const { return first(T * cum(u) / Q); }
+  // the last unit u with cum(u) <= m
+  __device__ int64_t unit_at(int64_t m) const { return m < K1 * R1 ? m / K1 : R1 + (m - K1 * R1) / K2; }
+  // the unit that takes position x: the last u with T cum(u) / Q <= cost(x)
+  __device__ int64_t unit_of(int64_t x) const { return unit_at(((cost(x) + 1) * Q - 1) / T); }
 };
 // Cost of a 64-row prefix position against any other position, in eighths: the 4x MFMA and
 // softmax work per chunk of the prefix tiles makes their units finish last under an even split
@@ -769,6 +777,13 @@ struct CostSplit {
 // Measured on C4's decode kernel, HBM-cold: weights 8 (even) 178.7 us, 9 170.6, 10 159.4,
 // 11 154.4, 12 155.5, 13 156.1, 14 156.4, 16 158.5.
 constexpr int64_t kPrefix64Cost = 11, kChunkCost = 8;
+// Shares of a first- and a second-round unit when a launch over E4M3 caches holds two
+// workgroups per CU: the first-dispatched workgroup of a CU ran ahead of the second (C2 over
+// E4M3, per-wave timeline: mean ends 82.5 and 101.3 us). HBM-cold, decode kernel, shares 1/1 ->
+// 4/3: C4 over E4M3 102.9 -> 98.6 us, C3's decode part 404 -> 401 us, C2 118 -> 117 us (9/7,
+// 3/2 and 5/3 no better). The 16-bit kernels at D = 64, also two per CU, ran the reference's
+// grid 2-7% slower with 4/3 and keep equal shares.
+constexpr int64_t kRound1Share = 4, kRound2Share = 3;
 
 constexpr int kPlanThreads = 256;    // the decode kernel's workgroup
 constexpr int kPlanLdsSeqs = 1024;  // flat starts kept in LDS for the unit search (else global)
@@ -970,7 +985,15 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int gw = (blockIdx.x - (p.PLAN ? 1 : 0)) * kWavesPerWG + wave;
-  const int unit = gw / p.HGW, hw = gw % p.HGW;
+  const int unit = gw / p.HGW;
+  // With two workgroups per CU, the second-round units (unit >= R1, each sharing its CUs with
+  // a first-round unit) take the two head halves the other way round, so every CU reads both
+  // halves of the token rows: a workgroup reading the first half of E4M3 rows (1 KB, heads 0-3)
+  // ran ~11% slower than one reading the second, whichever XCD it sat on and with the data's
+  // heads rotated, and a CU holding two of them set the launch. HBM-cold, decode kernel: C2
+  // over E4M3 122.1 -> 118.3 us, C4 105.4 -> 102.5, C3's decode part 417 -> 405; the
+  // reference's D = 64 grid 3-4% faster at its large points; one workgroup per CU unchanged.
+  const int hw = (gw % p.HGW) ^ (p.HGW == 8 && p.R1 < p.NU && unit >= p.R1 ? 4 : 0);
   const int NHG = p.Hkv / p.HGW;
 
   // This unit's merge job: none unless it owns a split segment (below). Written on every
@@ -1005,7 +1028,9 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
   const int64_t NUa = active_units(C, p.NU);
   if (unit >= NUa) return;
   const bool weighted = NX > 1 && P > 0;
-  const CostSplit split(P, C, NUa, weighted ? kPrefix64Cost : 1, weighted ? kChunkCost : 1);
+  const bool rounds = KV8 && p.R1 < NUa;  // E4M3, two workgroups per CU: second-round shares
+  const CostSplit split(P, C, NUa, weighted ? kPrefix64Cost : 1, weighted ? kChunkCost : 1, p.R1,
+                        rounds ? kRound1Share : 1, rounds ? kRound2Share : 1);
   const int64_t a = split.begin(unit), b = split.begin(unit + 1);
   if (a >= b) return;
 
@@ -2254,7 +2279,8 @@ static int launch_decode_nt(PAParams& p, hipStream_t s) {
   const void* k = (const void*)&pa_decode_kernel<E, D, NT, KV8, NX>;
   const int plan_wgs = p.PLAN ? 1 : 0;  // workgroup 0 plans the prefill launch
   int per_cu = 1;
-  int waves = (resident_blocks(k, 256, &per_cu) - plan_wgs) * kWavesPerWG;
+  const int resident = resident_blocks(k, 256, &per_cu);
+  int waves = (resident - plan_wgs) * kWavesPerWG;
   if (waves > kMaxDecodeWaves) waves = kMaxDecodeWaves;
   int64_t units = waves / p.HGW;
   // 16-bit caches: half the resident waves. Each split segment leaves one fp32 partial per
@@ -2284,6 +2310,11 @@ static int launch_decode_nt(PAParams& p, hipStream_t s) {
   if (units < 1) units = 1;
   p.NU = (int32_t)units;
   const int wgs = (p.NU * p.HGW + kWavesPerWG - 1) / kWavesPerWG;
+  // units whose last workgroup is dispatched before every CU holds one (unit u's waves are
+  // u HGW .. (u + 1) HGW - 1, behind the planning workgroup)
+  const int cus = per_cu > 0 ? resident / per_cu : resident;
+  const int64_t r1 = (int64_t)kWavesPerWG * (cus - plan_wgs) / p.HGW;
+  p.R1 = (int32_t)(wgs + plan_wgs > cus ? (r1 < 0 ? 0 : (r1 < units ? r1 : units)) : units);
   hipLaunchKernelGGL((pa_decode_kernel<E, D, NT, KV8, NX>), dim3(wgs + plan_wgs), dim3(256), 0, s, p);
   return (int)hipGetLastError();
 }

@@ -582,12 +582,13 @@ def test_prefill_priority_change_points_match_the_per_chunk_level():
                     assert lvl == lvl_of(i, n, rest, total), (total, n, rest, i)
 
 
-def test_cascade_cost_split_partitions_the_positions():
-    """The decode kernel's stream-K split by cost (`CostSplit`: the first P positions cost wp,
-    the others wr) must give every position of [0, C) to exactly one unit, units in order, and
-    `unit_of` must name the unit whose range holds each position (the merge records list a
-    segment's pieces by it). Weights 1/1 must give the plain split [u C / NUa, (u + 1) C / NUa).
-    The expressions are taken from the source and checked against a walk over every position."""
+def test_decode_cost_split_partitions_the_positions():
+    """The decode kernel's stream-K split (`CostSplit`: the first P positions cost wp, the others
+    wr; the first R1 units take K1 parts of the total cost, the others K2) must give every
+    position of [0, C) to exactly one unit, units in order, and `unit_of` must name the unit
+    whose range holds each position (the merge records list a segment's pieces by it). Costs
+    and shares 1 must give the plain split [u C / NUa, (u + 1) C / NUa). The expressions are
+    taken from the source and checked against a walk over every position."""
     src = (Path(__file__).resolve().parent.parent / "kvserve_amd/csrc/paged_attention.hip").read_text()
     body = re.search(r"struct CostSplit \{(.*?)\n\};", src, re.S).group(1)
 
@@ -599,32 +600,35 @@ def test_cascade_cost_split_partitions_the_positions():
             e = f"({a}) if ({cond}) else ({b})"
         return e.replace("/", "//")
 
-    cost_e, first_e, begin_e, unit_e = expr("cost"), expr("first"), expr("begin"), expr("unit_of")
-    prefix_w = int(re.search(r"constexpr int64_t kPrefix64Cost = (\d+), kChunkCost = (\d+);", src).group(1))
-    chunk_w = int(re.search(r"constexpr int64_t kPrefix64Cost = (\d+), kChunkCost = (\d+);", src).group(2))
+    fns = [(name, expr(name), arg) for name, arg in
+           (("cost", "x"), ("first", "c"), ("cum", "u"), ("begin", "u"), ("unit_at", "m"), ("unit_of", "x"))]
+    consts = dict(re.findall(r"constexpr int64_t (kPrefix64Cost|kChunkCost|kRound1Share|kRound2Share) = (\d+)", src))
+    consts.update(re.findall(r", (kChunkCost|kRound2Share) = (\d+);", src))
+    weights = [(1, 1), (int(consts["kPrefix64Cost"]), int(consts["kChunkCost"]))]
+    shares = [(1, 1), (int(consts["kRound1Share"]), int(consts["kRound2Share"])), (5, 4)]
 
-    def split(P, C, NUa, wp, wr):
+    def split(P, C, NUa, wp, wr, R1, K1, K2):
         env = {"P": P, "C": C, "NUa": NUa, "wp": wp, "wr": wr, "T": wp * P + wr * (C - P)}
-        f = {}
-        for name, e, arg in (("cost", cost_e, "x"), ("first", first_e, "c")):
-            f[name] = eval(f"lambda {arg}: {e}", dict(env))  # noqa: S307
-        env.update(f)
-        begin = eval(f"lambda u: {begin_e}", env)  # noqa: S307 (source text of this repo)
-        unit_of = eval(f"lambda x: {unit_e}", env)  # noqa: S307
-        return begin, unit_of
+        R1 = min(R1, NUa)
+        env.update({"R1": R1, "K1": K1, "K2": K2, "Q": K1 * R1 + K2 * (NUa - R1)})
+        for name, e, arg in fns:  # each may call the ones before it
+            env[name] = eval(f"lambda {arg}: {e}", env)  # noqa: S307 (source text of this repo)
+        return env["begin"], env["unit_of"]
 
     rng = random.Random(5)
     cases = [(0, 1, 1), (3, 3, 2), (375, 6375, 128)] + [
-        (rng.randint(0, c), c, rng.randint(1, 300)) for c in (rng.randint(1, 4000) for _ in range(400))
+        (rng.randint(0, c), c, rng.randint(1, 300)) for c in (rng.randint(1, 4000) for _ in range(300))
     ]
     for P, C, NUa in cases:
-        for wp, wr in ((1, 1), (prefix_w, chunk_w)):
-            begin, unit_of = split(P, C, NUa, wp, wr)
-            assert begin(0) == 0 and begin(NUa) == C, (P, C, NUa, wp, wr)
-            for u in range(NUa):
-                a, b = begin(u), begin(u + 1)
-                assert a <= b
-                if wp == wr == 1:
-                    assert a == u * C // NUa
-                for x in range(a, b):
-                    assert unit_of(x) == u, (P, C, NUa, wp, wr, u, x)
+        R1 = rng.choice([NUa, NUa // 2, rng.randint(0, NUa)])
+        for wp, wr in weights:
+            for K1, K2 in shares:
+                begin, unit_of = split(P, C, NUa, wp, wr, R1, K1, K2)
+                assert begin(0) == 0 and begin(NUa) == C, (P, C, NUa, wp, wr, R1, K1, K2)
+                for u in range(NUa):
+                    a, b = begin(u), begin(u + 1)
+                    assert a <= b
+                    if wp == wr == K1 == K2 == 1:
+                        assert a == u * C // NUa
+                    for x in range(a, b):
+                        assert unit_of(x) == u, (P, C, NUa, wp, wr, R1, K1, K2, u, x)
