@@ -615,12 +615,17 @@ def test_decode_cost_split_partitions_the_positions():
             env[name] = eval(f"lambda {arg}: {e}", env)  # noqa: S307 (source text of this repo)
         return env["begin"], env["unit_of"]
 
+    # the kernel's active units: at most ceil(C / kMinUnitChunks) (active_units)
+    internal = (Path(__file__).resolve().parent.parent / "kvserve_amd/csrc/kvh_internal.h").read_text()
+    min_chunks = int(re.search(r"kMinUnitChunks = (\d+);", internal + src).group(1))
+
     rng = random.Random(5)
     cases = [(0, 1, 1), (3, 3, 2), (375, 6375, 128)] + [
         (rng.randint(0, c), c, rng.randint(1, 300)) for c in (rng.randint(1, 4000) for _ in range(300))
     ]
     for P, C, NUa in cases:
         R1 = rng.choice([NUa, NUa // 2, rng.randint(0, NUa)])
+        active = NUa <= -(-C // min_chunks)
         for wp, wr in weights:
             for K1, K2 in shares:
                 begin, unit_of = split(P, C, NUa, wp, wr, R1, K1, K2)
@@ -630,5 +635,10 @@ def test_decode_cost_split_partitions_the_positions():
                     assert a <= b
                     if wp == wr == K1 == K2 == 1:
                         assert a == u * C // NUa
+                    # a segment's pieces sit on consecutive units, one each, and the merge reads
+                    # every one: at the kernel's unit counts and the source's weights and shares
+                    # (one kind at a time, as the kernel uses them) no unit may be empty
+                    if active and (wp, wr) in weights and (K1, K2) in shares[:2] and (wp == wr or K1 == K2):
+                        assert a < b, ("empty unit", P, C, NUa, wp, wr, R1, K1, K2, u)
                     for x in range(a, b):
                         assert unit_of(x) == u, (P, C, NUa, wp, wr, R1, K1, K2, u, x)
