@@ -22,6 +22,8 @@ Also printed in the same JSON line:
                  the 8 TB/s HBM peak; `traffic` is the kernel's HBM bytes per launch from two
                  child rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) calibrated on a plain
                  copy of known size;
+  roofline_prefill - the same for C3's prefill kernel against the dense bf16 MFMA peak, its
+                 `traffic` from the same two passes over a C3 child;
   cpu_baseline - the torch restatement of the reference's TorchAttention.forward (fp32, the
                  host's cores) on a bounded sample of the same workload;
   secondary    - the other BASELINE configs (C1, C3 prefill TFLOP/s + decode GB/s, C4 on
@@ -579,10 +581,10 @@ def pmc_child(idx: int = 2, fp8: bool = False) -> None:
     torch.cuda.synchronize()
 
 
-def measure_traffic(timeout_s: int = 150) -> dict | None:
-    """HBM bytes per decode-kernel launch from two rocprofv3 --pmc passes (FETCH_SIZE, then
-    WRITE_SIZE, KiB per dispatch), each scaled by what the same counter reads for the
-    calibration copy of known size. None when rocprofv3 is missing or a pass fails."""
+def measure_traffic(timeout_s: int = 150, idx: int = 2, kernel: str = "pa_decode_kernel") -> dict | None:
+    """HBM bytes per launch of `kernel` in BASELINE config `idx` from two rocprofv3 --pmc passes
+    (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the same counter reads
+    for the calibration copy of known size. None when rocprofv3 is missing or a pass fails."""
     import csv
     import shutil
     import subprocess
@@ -596,7 +598,7 @@ def measure_traffic(timeout_s: int = 150) -> dict | None:
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
         d = tempfile.mkdtemp(prefix="kvh_pmc_", dir="/tmp")
         cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "pmc", "--",
-               sys.executable, str(ROOT / "bench.py"), "--pmc-child"]  # fmt: skip
+               sys.executable, str(ROOT / "bench.py"), "--pmc-child", "--only", str(idx)]  # fmt: skip
         env = dict(os.environ, TMPDIR="/tmp")
         try:
             subprocess.run(cmd, cwd="/tmp", env=env, timeout=timeout_s, check=True,
@@ -612,7 +614,7 @@ def measure_traffic(timeout_s: int = 150) -> dict | None:
                 name, val = row["Kernel_Name"], float(row["Counter_Value"]) * 1024.0
                 if "neg_kernel" in name:
                     calib.append(val)
-                elif "pa_decode_kernel" in name:
+                elif kernel in name:
                     dec.append(val)
         shutil.rmtree(d, ignore_errors=True)
         if not calib or not dec:
@@ -634,7 +636,7 @@ def main() -> int:
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", type=int, default=0, help="run just this config (1-5) and print its record")
     p.add_argument("--fp8", action="store_true", help="with --only: E4M3 KV caches")
-    p.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
+    p.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc passes")
     p.add_argument("--no-engine", action="store_true", help="skip the 1B/8B engine decode tokens/s")
     p.add_argument("--engine-only", action="store_true", help="run just the engine decode tokens/s")
     p.add_argument("--probes", action="store_true",
@@ -754,6 +756,15 @@ def main() -> int:
                 "workload": "c3_mixed_prefill: the 4 prefill chunks of 384 tokens (HBM-cold, median)",
                 "gflop": c3["prefill_gflop"],
             }
+            if not args.no_traffic:
+                # what the prefill kernel moves: Q, the K/V chunks of its tiles (re-read by the
+                # units that split a tile), its output rows and the split tiles' fp32 partials
+                t = measure_traffic(idx=3, kernel="pa_prefill_kernel")
+                if t is not None:
+                    rp = record["roofline_prefill"]
+                    rp["traffic"] = t["FETCH_SIZE"]["bytes"] + t["WRITE_SIZE"]["bytes"]
+                    rp["traffic_detail"] = {"fetch_bytes": t["FETCH_SIZE"]["bytes"], "write_bytes": t["WRITE_SIZE"]["bytes"]}
+                print(f"# prefill traffic: {t}", file=sys.stderr, flush=True)
     if not args.no_secondary:
         meta = {}
         for idx in (2, 3):
