@@ -12,6 +12,7 @@ oracle (oracle/fp8.py):
 from __future__ import annotations
 
 import dataclasses
+import random
 
 import pytest
 import torch
@@ -181,6 +182,26 @@ def test_split_decode_segments(hip_device):
     kc, vc = _fp8_caches(b, 2.0, 0.125)
     out = _attend_fp8(b, kc, vc, 2.0, 0.125)
     err = (out.float().cpu() - _oracle(b, kc, vc, 2.0, 0.125)).abs().max().item()
+    assert err <= pc.TOL_16BIT, err
+
+
+def test_partial_second_dispatch_round(hip_device):
+    """Tables 4096 keys wide over contexts of 120-260 tokens: the decode launch is sized from
+    the tables for two workgroups per CU (256 units, the first 128 in the first dispatch round),
+    but the chunks give only ~210 units work, so part of the second round is active. Its units
+    take the head halves the other way round and 3/4 of a first-round unit's share of the split;
+    every chunk must still reach exactly one unit and every head its own rows."""
+    rng = random.Random(17)
+    ctx = [rng.randint(120, 260) for _ in range(64)]
+    seq = [c + 1 for c in ctx]
+    pool = 20_000
+    tables = workloads._disjoint_tables(rng, seq, 16, pool)
+    w = workloads.Workload("fp8_round2", [1] * 64, seq, tables, pool, 32, 8, 128, 16, width=256)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=17)
+    kc, vc = _fp8_caches(b, 0.5, 1.0)
+    out = _attend_fp8(b, kc, vc, 0.5, 1.0)
+    assert last_launch_kernels() == ["decode", "reduce"], last_launch_kernels()
+    err = (out.float().cpu() - _oracle(b, kc, vc, 0.5, 1.0)).abs().max().item()
     assert err <= pc.TOL_16BIT, err
 
 

@@ -301,6 +301,24 @@ def test_split_k_matches_single_pass(hip_device):
     print("narrow:", k_narrow, "wide:", k_wide)
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_partial_second_dispatch_round(hip_device, dtype):
+    """D = 64, 16-bit caches: the decode kernel fits two workgroups per CU, so a launch sized
+    from 4096-key tables holds two dispatch rounds of units; contexts of 120-260 tokens give
+    only part of the second round work. Second-round units take the two halves of the 8-head
+    group the other way round from first-round units; every head must still get its own rows
+    (TorchAttention reads each sequence on its own, src/kvserve/attention.py:31-82)."""
+    rng = random.Random(23)
+    seq = [rng.randint(120, 260) + 1 for _ in range(64)]
+    pool = 20_000
+    tables = workloads._disjoint_tables(rng, seq, 16, pool)
+    w = workloads.Workload("round2", [1] * 64, seq, tables, pool, 32, 8, 64, 16, width=256)
+    b = workloads.materialize(w, dtype, hip_device, seed=23)
+    out = pc.attend(b)
+    assert last_launch_kernels() == ["decode", "reduce"], last_launch_kernels()
+    assert pc.max_err_vs_oracle(b, out, list(range(64))) <= pc.TOL_16BIT
+
+
 def test_mixed_batch_dispatch(hip_device):
     """Decode-class rows take the stream-K decode kernel and longer queries the prefill
     kernel (whose work plan the decode launch lays out), all launched over the same
