@@ -711,17 +711,25 @@ struct SeqWindow {
   int nexcl;  // cascade members blk0 .. blk0 + l - 1
   int ntotal; // cascade members of the whole window
   int mem;    // this lane's sequence is a cascade member
+  int qs, ql, ctx, kvt;  // this lane's SeqView (ctx clamped to [-q_len, kv_total])
 };
 
 __device__ __forceinline__ void scan_window(SeqWindow& sw, const PAParams& p, int blk0, int base, int nbase,
                                             int skip) {
   const int lane = threadIdx.x & 63;
   const int s = blk0 + lane;
-  int c = 0, mem = 0;
+  int c = 0, mem = 0, qs = 0, ql = 0, cx = 0, kt = 0;
   if (s < p.B) {
     const SeqView v = seq_view(p, s);
     c = seq_chunks(p, v, skip);
     mem = cascade_member(p, v) ? 1 : 0;
+    // 32-bit copies for the segment walk: qs <= T < 2^31 and kv_total < 2^31 (checked on the
+    // host); ctx is only read as clamp(ctx + qi + 1, 0, kv_total) for 0 <= qi < q_len and as
+    // clamp(ctx, 0, kv_total), which clamping it to [-q_len, kv_total] leaves unchanged
+    qs = (int)v.qs;
+    ql = v.q_len;
+    kt = v.kv_total;
+    cx = (int)clamp64(v.ctx, -(int64_t)v.q_len, v.kv_total);
   }
   int incl = c, ninc = mem;
 #pragma unroll
@@ -741,6 +749,10 @@ __device__ __forceinline__ void scan_window(SeqWindow& sw, const PAParams& p, in
   sw.nexcl = ninc - mem;
   sw.ntotal = __builtin_amdgcn_readlane(ninc, 63);
   sw.mem = mem;
+  sw.qs = qs;
+  sw.ql = ql;
+  sw.ctx = cx;
+  sw.kvt = kt;
 }
 
 __device__ __forceinline__ int64_t active_units(int64_t C, int NU) {
@@ -1076,7 +1088,14 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
     const int64_t y = b < seg_end ? b : seg_end;
     const int kvh = hg * p.HGW + hw;
 
-    const SeqView sv = seq_view(p, seq);
+    // the sequence's view from the window's lane l (no second, dependent read of the
+    // metadata before the query and page-table loads: C2 200.1 -> 198.9 us HBM-cold, C2 over
+    // E4M3 117.0 -> 115.9)
+    SeqView sv;
+    sv.qs = __builtin_amdgcn_readlane(sw.qs, l);
+    sv.q_len = __builtin_amdgcn_readlane(sw.ql, l);
+    sv.ctx = __builtin_amdgcn_readlane(sw.ctx, l);
+    sv.kv_total = __builtin_amdgcn_readlane(sw.kvt, l);
     const int R = sv.q_len * p.G;
     const bool member = L > 0 && __builtin_amdgcn_readlane(sw.mem, l);
     const int skip = member ? L : 0;
@@ -2285,9 +2304,10 @@ static int launch_decode_nt(PAParams& p, hipStream_t s) {
   int64_t units = waves / p.HGW;
   // 16-bit caches: half the resident waves. Each split segment leaves one fp32 partial per
   // unit (RS x D per wave), written here and read back by the merge; with half the units the
-  // pieces are twice as long and the partial traffic halves, while 4 waves per SIMD still
-  // keep HBM busy (measured HBM-cold, C2 5.46 -> 5.62 TB/s, C5 3.88 -> 4.20 TB/s; a quarter
-  // of the waves loses 10-20%). E4M3 caches convert every element before the MFMA and keep
+  // pieces are twice as long and the partial traffic halves, while the waves left (one per
+  // SIMD of the two the D = 128 kernels fit, two of four at D = 64) still keep HBM busy
+  // (measured HBM-cold, C2 5.46 -> 5.62 TB/s, C5 3.88 -> 4.20 TB/s; a quarter of the waves
+  // loses 10-20%). E4M3 caches convert every element before the MFMA and keep
   // two thirds (2 of the 3 waves per SIMD the kernel fits): with three, the last-dispatched
   // workgroups of each CU finish up to 50% later than the first (HBM-cold C2 2%, C4 4% slower
   // than with two), while half the waves is 5% slower. A kernel that fits one wave per SIMD
