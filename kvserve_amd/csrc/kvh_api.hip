@@ -79,17 +79,19 @@ Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t 
     // cascade over a shared prefix: share header, decode list, prefix partials, merge jobs
     pl.cascade = !pl.launch_prefill && pl.NT == 1 && B >= 2 && (int64_t)W * BS > kCascadeMinTokens;
     // A prefix group stacks the query rows of SG = XR / RS members into NX 16-row tiles
-    // (XR = 16 NX rows). Over 16-bit caches four tiles (64 rows) when the batch holds more
-    // than one tile's worth, so up to 64 / RS members read the shared K/V once; the E4M3
-    // kernel keeps one tile (its occupancy matters more than the prefix re-reads), so the
-    // partials are sized for either.
+    // (XR = 16 NX rows). When the batch holds more than one tile's worth: over 16-bit caches
+    // four tiles (64 rows), so up to 64 / RS members read the shared K/V once; over E4M3
+    // caches two (32 rows), the most that keeps the kernel at two waves per SIMD, which its
+    // conversions need (cascade_tiles). The partials are sized for every choice.
     pl.NX = pl.cascade && (int64_t)B * pl.RS > 16 ? 4 : 1;
     const int64_t nhg = Hkv / pl.HGW;
     auto prefix_rows = [&](int nx) {
       const int xr = 16 * nx, sg = cascade_group(pl.RS, nx);
       return (((int64_t)B + sg - 1) / sg * nhg + kMaxCascadeWaves / pl.HGW) * pl.HGW * xr;
     };
-    pl.xrows = pl.cascade ? std::max(prefix_rows(pl.NX), prefix_rows(1)) : 0;
+    pl.xrows = pl.cascade ? std::max({prefix_rows(cascade_tiles(pl.NX, false)), prefix_rows(cascade_tiles(pl.NX, true)),
+                                      prefix_rows(1)})
+                          : 0;
     pl.ws_x_bytes = pl.cascade ? align_up(kShareHdr * sizeof(int64_t)) + align_up((size_t)B * sizeof(int32_t)) +
                                      align_up((size_t)pl.xrows * D * sizeof(float)) +
                                      align_up((size_t)pl.xrows * 2 * sizeof(float)) +
@@ -414,7 +416,7 @@ static int paged_attention_impl(const void* q, int64_t q_tok_stride, int64_t q_h
   p.NUP = 0;  // set by the prefill launcher likewise
   p.CASC = 0;  // set by the launcher when the plan has the cascade path
   {
-    const int nx = kv8 ? 1 : plan.NX;  // cascade prefix group: 16-row tiles (see make_plan)
+    const int nx = cascade_tiles(plan.NX, kv8);  // cascade prefix group: 16-row tiles (see make_plan)
     p.XR = 16 * nx;
     p.SG = cascade_group(plan.RS, nx);
   }

@@ -107,6 +107,9 @@ struct Plan {
 
 // Cascade: decode-class sequences per prefix group of nx 16-row tiles, RS rows each.
 inline int32_t cascade_group(int32_t RS, int32_t nx) { return RS >= 16 * nx ? 1 : 16 * nx / RS; }
+// 16-row tiles of a cascade prefix group: the plan's NX (4 or 1) over 16-bit caches, at most 2
+// over E4M3 caches.
+inline int32_t cascade_tiles(int32_t NX, bool kv8) { return kv8 && NX > 2 ? 2 : NX; }
 
 Plan make_plan(int64_t T, int32_t B, int32_t H, int32_t Hkv, int32_t D, int32_t W, int32_t BS, int32_t max_q,
                int32_t dtype);

@@ -788,6 +788,8 @@ struct CostSplit {
 // (HBM-cold C4: units of prefix positions ended at 151-162 us, the others at 141-145 us).
 // Measured on C4's decode kernel, HBM-cold: weights 8 (even) 178.7 us, 9 170.6, 10 159.4,
 // 11 154.4, 12 155.5, 13 156.1, 14 156.4, 16 158.5.
+// The 32-row groups over E4M3 caches keep the even split (C4 over E4M3, HBM-cold: weights 7
+// 92.7 us, 8 91.3, 9 92.3, 10 93.4, 12 96.0).
 constexpr int64_t kPrefix64Cost = 11, kChunkCost = 8;
 // Shares of a first- and a second-round unit when a launch over E4M3 caches holds two
 // workgroups per CU: the first-dispatched workgroup of a CU ran ahead of the second (C2 over
@@ -1039,7 +1041,7 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
   const int64_t C = P + (int64_t)Cs * NHG;
   const int64_t NUa = active_units(C, p.NU);
   if (unit >= NUa) return;
-  const bool weighted = NX > 1 && P > 0;
+  const bool weighted = NX == 4 && P > 0;
   const bool rounds = KV8 && p.R1 < NUa;  // E4M3, two workgroups per CU: second-round shares
   const CostSplit split(P, C, NUa, weighted ? kPrefix64Cost : 1, weighted ? kChunkCost : 1, p.R1,
                         rounds ? kRound1Share : 1, rounds ? kRound2Share : 1);
@@ -1059,9 +1061,10 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
       WaveState<D, NX> st;
       load_q_group<D, NX, KV8>(st, p, grp, nd, L, kvh);
       const int64_t* btrow = p.bt + (int64_t)r0 * p.bt_rs;
-      // 16-row groups (NX = 1) each read the shared keys: ordinary loads, so the other groups'
-      // reads hit the Infinity Cache (non-temporal ones ran C4 over E4M3 103 -> 108 us)
-      run_chunks<E, D, NX, KV8, (NX > 1)>(st, p, btrow, kvh, (int)(pos - seg_beg) * kChunk, kChunk,
+      // 16- and 32-row groups each read the shared keys: ordinary loads, so the other groups'
+      // reads hit the Infinity Cache (non-temporal ones ran C4 over E4M3 103 -> 108 us with
+      // 16-row groups)
+      run_chunks<E, D, NX, KV8, (NX > 2)>(st, p, btrow, kvh, (int)(pos - seg_beg) * kChunk, kChunk,
                                           (int)(y - seg_beg) * kChunk, L);
       SeqView none{};
       write_rows<E, D, NX>(st, p, none, 16 * NX, 0, kvh, true, p.ws_xacc, p.ws_xml,
@@ -2310,13 +2313,13 @@ static int launch_decode_nt(PAParams& p, hipStream_t s) {
   // loses 10-20%). E4M3 caches convert every element before the MFMA and keep
   // two thirds (2 of the 3 waves per SIMD the kernel fits): with three, the last-dispatched
   // workgroups of each CU finish up to 50% later than the first (HBM-cold C2 2%, C4 4% slower
-  // than with two), while half the waves is 5% slower. A kernel that fits one wave per SIMD
-  // (the 64-row cascade tiles, 48 or 64 verify rows) keeps them all: halving would idle
-  // half the CUs.
+  // than with two), while half the waves is 5% slower; the 32-row cascade instance over E4M3
+  // fits two per SIMD and keeps both. A kernel that fits one wave per SIMD (the 64-row cascade
+  // tiles, 48 or 64 verify rows) keeps them all: halving would idle half the CUs.
   if (per_cu >= 2) {
     if (!KV8)
       units /= 2;
-    else
+    else if (!(NX > 1 && per_cu == 2))
       units = units * 2 / 3;
   }
   if (p.CASC && units > kMaxCascadeWaves / p.HGW) units = kMaxCascadeWaves / p.HGW;  // prefix partial slots
@@ -2368,8 +2371,13 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipSt
   switch (plan.NT) {
     case 1:
       if constexpr (!KV8) {
-        if (plan.cascade && p.XR == 64) {  // 64-row prefix groups (16-bit caches only)
+        if (plan.cascade && p.XR == 64) {  // 64-row prefix groups (16-bit caches)
           err = launch_decode_nt<E, D, 1, KV8, 4>(p, s);
+          break;
+        }
+      } else {
+        if (plan.cascade && p.XR == 32) {  // 32-row prefix groups (E4M3 caches)
+          err = launch_decode_nt<E, D, 1, KV8, 2>(p, s);
           break;
         }
       }

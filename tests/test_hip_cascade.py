@@ -2,11 +2,12 @@
 start with the same physical blocks, configs[3] of BASELINE.json): the shared keys are computed
 once per group of sequences and merged with each sequence's own keys. The output must match
 the oracle as for any other batch (TorchAttention reads every sequence's table on its own,
-src/kvserve/attention.py:31-82); the cases vary the group shape (SG = 64 / (q_len G)
-sequences per 64-row group over 16-bit caches when the batch has more than 16 rows, else
-16 / (q_len G) per 16-row group, and always 16-row groups over E4M3 caches: one group of 16
-in g4_b16, two in g4_b23_ragged, one at D = 64 in d64_bs16_b9, 16-row groups in g1_b5_sg16
-and d64_bs32_b2, 4 and 5 members of 16 and 12 rows in g8_q2_sg1 and g4_q3_rs12), where the
+src/kvserve/attention.py:31-82); the cases vary the group shape (when the batch has more than
+16 rows, SG = 64 / (q_len G) sequences per 64-row group over 16-bit caches and 32 / (q_len G)
+per 32-row group over E4M3 caches, else 16 / (q_len G) per 16-row group: over 16-bit caches
+one group of 16 in g4_b16, two in g4_b23_ragged, one at D = 64 in d64_bs16_b9, 16-row groups
+in g1_b5_sg16 and d64_bs32_b2, 4 and 5 members of 16 and 12 rows in g8_q2_sg1 and
+g4_q3_rs12; over E4M3 caches two 32-row groups in g4_b16, three in g4_b23_ragged), where the
 sharing stops (a diverging table, the shortest member context), members that do not join
 (padding rows, short contexts), E4M3 caches and graph replays whose metadata switches the
 cascade on and off.
@@ -153,9 +154,22 @@ def test_shortest_member_limits_the_shared_length(hip_device):
 
 @pytest.mark.parametrize("k_scale,v_scale", [(1.0, 1.0), (0.5, 2.0)])
 def test_shared_prefix_fp8(hip_device, k_scale, v_scale):
-    q, c, heads, D, BS, shared, width = CASES["g4_b16"]
-    w = shared_workload(q, c, heads, D, BS, shared, width, seed=5)
-    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=5)
+    _fp8_case(hip_device, "g4_b16", k_scale, v_scale, seed=5)
+
+
+@pytest.mark.parametrize("name", ["g4_b23_ragged", "g4_q3_rs12", "g8_q2_sg1", "d64_bs16_b9", "g1_b5_sg16", "d64_bs32_b2"])
+def test_shared_prefix_fp8_groups(hip_device, name):
+    """E4M3 caches stack a batch of more than 16 rows into 32-row prefix groups (two tiles per
+    wave): three groups of 8 members with a ragged last one, 2 members of 12 rows, 2 of 16
+    rows with padding rows between mixed query lengths, D = 64; batches of at most 16 rows keep
+    one 16-row group."""
+    _fp8_case(hip_device, name, 0.5, 2.0, seed=13)
+
+
+def _fp8_case(hip_device, name, k_scale, v_scale, seed):
+    q, c, heads, D, BS, shared, width = CASES[name]
+    w = shared_workload(q, c, heads, D, BS, shared, width, seed=seed)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=seed)
     kc = fp8.quantize(b.k_cache, k_scale).to(hip_device)
     vc = fp8.quantize(b.v_cache, v_scale).to(hip_device)
     HipAttention.write_kv(kc, vc, b.k_new, b.v_new, b.meta.slot_mapping, k_scale=k_scale, v_scale=v_scale)

@@ -604,8 +604,13 @@ def test_decode_cost_split_partitions_the_positions():
            (("cost", "x"), ("first", "c"), ("cum", "u"), ("begin", "u"), ("unit_at", "m"), ("unit_of", "x"))]
     consts = dict(re.findall(r"constexpr int64_t (kPrefix64Cost|kChunkCost|kRound1Share|kRound2Share) = (\d+)", src))
     consts.update(re.findall(r", (kChunkCost|kRound2Share) = (\d+);", src))
-    weights = [(1, 1), (int(consts["kPrefix64Cost"]), int(consts["kChunkCost"]))]
-    shares = [(1, 1), (int(consts["kRound1Share"]), int(consts["kRound2Share"])), (5, 4)]
+    w64 = (int(consts["kPrefix64Cost"]), int(consts["kChunkCost"]))
+    weights = [(1, 1), w64, (10, 8)]
+    rounds = (int(consts["kRound1Share"]), int(consts["kRound2Share"]))
+    shares = [(1, 1), rounds, (5, 4)]
+    # (weights, shares) as the kernel combines them: 64-row prefix groups (16-bit caches: no
+    # round shares), E4M3 caches (shares, even costs); and weights with shares together
+    used = {((1, 1), (1, 1)), (w64, (1, 1)), ((1, 1), rounds), (w64, rounds), ((10, 8), rounds)}
 
     def split(P, C, NUa, wp, wr, R1, K1, K2):
         env = {"P": P, "C": C, "NUa": NUa, "wp": wp, "wr": wr, "T": wp * P + wr * (C - P)}
@@ -623,6 +628,8 @@ def test_decode_cost_split_partitions_the_positions():
     cases = [(0, 1, 1), (3, 3, 2), (375, 6375, 128)] + [
         (rng.randint(0, c), c, rng.randint(1, 300)) for c in (rng.randint(1, 4000) for _ in range(300))
     ]
+    # every small shape at the kernel's unit counts (NUa <= ceil(C / kMinUnitChunks))
+    cases += [(P, C, NUa) for C in range(1, 19) for P in range(C + 1) for NUa in range(1, -(-C // min_chunks) + 1)]
     for P, C, NUa in cases:
         R1 = rng.choice([NUa, NUa // 2, rng.randint(0, NUa)])
         active = NUa <= -(-C // min_chunks)
@@ -637,8 +644,8 @@ def test_decode_cost_split_partitions_the_positions():
                         assert a == u * C // NUa
                     # a segment's pieces sit on consecutive units, one each, and the merge reads
                     # every one: at the kernel's unit counts and the source's weights and shares
-                    # (one kind at a time, as the kernel uses them) no unit may be empty
-                    if active and (wp, wr) in weights and (K1, K2) in shares[:2] and (wp == wr or K1 == K2):
+                    # (in the combinations the kernel uses) no unit may be empty
+                    if active and ((wp, wr), (K1, K2)) in used:
                         assert a < b, ("empty unit", P, C, NUa, wp, wr, R1, K1, K2, u)
                     for x in range(a, b):
                         assert unit_of(x) == u, (P, C, NUa, wp, wr, R1, K1, K2, u, x)
