@@ -2313,13 +2313,15 @@ static int launch_decode_nt(PAParams& p, hipStream_t s) {
   // loses 10-20%). E4M3 caches convert every element before the MFMA and keep
   // two thirds (2 of the 3 waves per SIMD the kernel fits): with three, the last-dispatched
   // workgroups of each CU finish up to 50% later than the first (HBM-cold C2 2%, C4 4% slower
-  // than with two), while half the waves is 5% slower; the 32-row cascade instance over E4M3
-  // fits two per SIMD and keeps both. A kernel that fits one wave per SIMD (the 64-row cascade
-  // tiles, 48 or 64 verify rows) keeps them all: halving would idle half the CUs.
+  // than with two), while half the waves is 5% slower. An E4M3 kernel that fits two waves per
+  // SIMD (the two-tile verify rows, the 32-row cascade tiles) keeps both: C5 over E4M3 decode
+  // 64.8 -> 58.1 us HBM-cold against two thirds of them. A kernel that fits one wave per SIMD
+  // (the 64-row cascade tiles, 48 or 64 verify rows) keeps them all: halving would idle half
+  // the CUs.
   if (per_cu >= 2) {
     if (!KV8)
       units /= 2;
-    else if (!(NX > 1 && per_cu == 2))
+    else if (per_cu >= 3)
       units = units * 2 / 3;
   }
   if (p.CASC && units > kMaxCascadeWaves / p.HGW) units = kMaxCascadeWaves / p.HGW;  // prefix partial slots
