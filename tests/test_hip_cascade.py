@@ -184,30 +184,36 @@ def _fp8_case(hip_device, name, k_scale, v_scale, seed):
     assert err <= pc.TOL_16BIT, err
 
 
-def test_graph_replays_switch_the_cascade(hip_device):
+@pytest.mark.parametrize("fp8_cache", [False, True], ids=["bf16", "e4m3"])
+def test_graph_replays_switch_the_cascade(hip_device, fp8_cache):
     """One captured forward replayed over metadata edited in place: shared tables (prefix
-    segments), then one table diverging at column 0 (no sharing, plain records), then shared
-    again with other lengths; every replay equals the eager call on the same metadata."""
+    segments: one 64-row group over bf16 caches, two 32-row groups over E4M3 caches), then one
+    table diverging at column 0 (no sharing, plain records), then shared again with other
+    lengths; every replay equals the eager call on the same metadata."""
     q, c, heads, D, BS, shared, width = CASES["g4_b16"]
     w = shared_workload(q, c, heads, D, BS, shared, width, seed=9)
     b = workloads.materialize(w, torch.bfloat16, hip_device, seed=9)
-    HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping)
+    kw = {"k_scale": 0.5, "v_scale": 2.0} if fp8_cache else {}
+    if fp8_cache:
+        b.k_cache = fp8.quantize(b.k_cache, kw["k_scale"]).to(hip_device)
+        b.v_cache = fp8.quantize(b.v_cache, kw["v_scale"]).to(hip_device)
+    HipAttention.write_kv(b.k_cache, b.v_cache, b.k_new, b.v_new, b.meta.slot_mapping, **kw)
     m = b.meta
     out = torch.empty_like(b.q)
 
-    def fwd():
-        return HipAttention.forward(b.q, b.k_cache, b.v_cache, m, w.scale, out=out)
+    def fwd(**extra):
+        return HipAttention.forward(b.q, b.k_cache, b.v_cache, m, w.scale, **kw, **extra)
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         for _ in range(2):
-            fwd()
+            fwd(out=out)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        fwd()
+        fwd(out=out)
 
     bt0 = m.block_tables.clone()
     sl0 = m.seq_lens.clone()
@@ -222,9 +228,16 @@ def test_graph_replays_switch_the_cascade(hip_device):
         torch.cuda.synchronize()
         got = out.clone()
         torch.randn(1 << 20, device=hip_device).sum()  # eager work between replays
-        eager = HipAttention.forward(b.q, b.k_cache, b.v_cache, m, w.scale)
+        eager = fwd()
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), eager.view(torch.int16)), i
     # the last state against the oracle (seq_lens shortened: fresh workload view of it)
     w.seq_lens = m.seq_lens.tolist()
-    _check(b, got)
+    if not fp8_cache:
+        _check(b, got)
+        return
+    ref = torch_reference.forward(
+        b.q.float().cpu(), fp8.dequantize(b.k_cache.cpu(), kw["k_scale"]), fp8.dequantize(b.v_cache.cpu(), kw["v_scale"]),
+        m.block_tables.cpu(), m.seq_lens.cpu(), m.query_lens.cpu(), w.scale,
+    )  # fmt: skip
+    assert (got.float().cpu() - ref).abs().max().item() <= pc.TOL_16BIT
