@@ -7,7 +7,8 @@ src/kvserve/attention.py:31-82); the cases vary the group shape (when the batch 
 per 32-row group over E4M3 caches, else 16 / (q_len G) per 16-row group: over 16-bit caches
 one group of 16 in g4_b16, two in g4_b23_ragged, one at D = 64 in d64_bs16_b9, 16-row groups
 in g1_b5_sg16 and d64_bs32_b2, 4 and 5 members of 16 and 12 rows in g8_q2_sg1 and
-g4_q3_rs12; over E4M3 caches two 32-row groups in g4_b16, three in g4_b23_ragged), where the
+g4_q3_rs12, 5 members in g4_b5_partial; over E4M3 caches two 32-row groups in g4_b16, three in
+g4_b23_ragged, one of 5 members in g4_b5_partial), where the
 sharing stops (a diverging table, the shortest member context), members that do not join
 (padding rows, short contexts), E4M3 caches and graph replays whose metadata switches the
 cascade on and off.
@@ -70,6 +71,7 @@ CASES = {
     "g8_q2_sg1": ([2, 1, 2, 2, 1, 2, 1, 1, 2], [1000 + 97 * i for i in range(9)], (32, 4), 128, 16, 40, 600),
     "g4_q3_rs12": ([3, 1, 2, 3, 3, 1], [800, 1900, 600, 1500, 1000, 3000], (32, 8), 128, 16, 30, 600),
     "g4_b23_ragged": ([1] * 23, [300 + 211 * i for i in range(23)], (32, 8), 128, 16, 18, 800),
+    "g4_b5_partial": ([1] * 5, [900, 1700, 2500, 1200, 3100], (32, 8), 128, 16, 40, 600),
 }
 
 
@@ -157,12 +159,14 @@ def test_shared_prefix_fp8(hip_device, k_scale, v_scale):
     _fp8_case(hip_device, "g4_b16", k_scale, v_scale, seed=5)
 
 
-@pytest.mark.parametrize("name", ["g4_b23_ragged", "g4_q3_rs12", "g8_q2_sg1", "d64_bs16_b9", "g1_b5_sg16", "d64_bs32_b2"])
+@pytest.mark.parametrize(
+    "name", ["g4_b23_ragged", "g4_q3_rs12", "g8_q2_sg1", "d64_bs16_b9", "g4_b5_partial", "g1_b5_sg16", "d64_bs32_b2"]
+)
 def test_shared_prefix_fp8_groups(hip_device, name):
     """E4M3 caches stack a batch of more than 16 rows into 32-row prefix groups (two tiles per
     wave): three groups of 8 members with a ragged last one, 2 members of 12 rows, 2 of 16
-    rows with padding rows between mixed query lengths, D = 64; batches of at most 16 rows keep
-    one 16-row group."""
+    rows with padding rows between mixed query lengths, D = 64, one group of 5 members (20 of
+    its 32 rows); batches of at most 16 rows keep one 16-row group."""
     _fp8_case(hip_device, name, 0.5, 2.0, seed=13)
 
 
