@@ -70,7 +70,7 @@ struct PAParams {
   int32_t PLAN;    // 1: workgroup 0 of the decode launch writes the prefill plan
   int32_t CASC;    // 1: the share kernel ran before the decode launch (cascade over a shared prefix)
   int32_t SG;      // cascade: decode-class sequences per prefix group (XR / RS)
-  int32_t XR;      // cascade: query rows per prefix group tile (16 NX: 16 or 64)
+  int32_t XR;      // cascade: query rows per prefix group tile (16 NX: 16, 32 or 64)
   int32_t R1;      // decode: units whose workgroups all sit in the first dispatch round (one per CU)
   int32_t PR;      // query rows ((token, head) pairs of one kv head) per prefill tile
   float v_scale;   // factor of every output row: the V scale of an E4M3 cache, else 1

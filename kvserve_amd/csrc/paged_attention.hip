@@ -613,13 +613,35 @@ __device__ __forceinline__ SeqView seq_view_uniform(const PAParams& p, int seq) 
   return v;
 }
 
+// Float offset of float4 c4 of row r in a head's group of `cap` partial rows (one split
+// piece's fp32 accumulators, written by write_rows, read by the merge) in the tile-block
+// layout (launches over E4M3 caches: write_rows<..., BLK> and merge_job<..., BLK>). The rows
+// are kept in 16-row tiles in the order the accumulator lanes hold them: lane (j, n) of a tile
+// holds row n, d = VW (4j + e) + i, i.e. float4 c4 = VW j + k with k = e VW / 4 + i / 4, and
+// that float4 lies at
+// (k * 4 + j) * m + n of the tile's m-row block (m = min(16, cap - 16 t)). Each store
+// instruction of a wave (one k) then writes 64 m contiguous bytes; with rows laid out whole it
+// writes 16 bytes to each of 4 lines of every row. HBM-cold, three runs each: C5 over E4M3
+// (two row tiles) decode 58.2 -> 50.3 us, merge 10.8 -> 11.9; single-tile rows over E4M3 (C2,
+// C4) gained 0.3-0.6 us in the decode kernel and lost 0.6-1.3 us in the merge, and over
+// 16-bit caches the decode kernels gained at most 0.8 us and the merges lost up to 1.0, so
+// those keep whole rows: the layout is used by multi-tile rows over E4M3 caches only.
+template <int D>
+__device__ __forceinline__ int part_ofs(int r, int c4, int cap) {
+  constexpr int VW = D / 16;
+  const int t = r >> 4, n = r & 15, m = min(16, cap - 16 * t);
+  return 16 * t * D + (((c4 % VW) * 4 + c4 / VW) * m + n) * 4;
+}
+
 // Writes one wave's result for its 16-row tiles: the normalised output row, or (partial)
-// the unnormalised acc, running max m and sum l of a piece of a split segment, at
-// ws row index row_base + r. Lane (j, n) holds row row0 + 16t + n, d = VW (4j + e) + i.
-template <class E, int D, int NT>
+// the unnormalised acc (BLK: laid out by part_ofs in the head's cap-row group starting at ws
+// row row_base; else whole rows at ws row row_base + r), running max m and sum l of a piece of
+// a split segment (at ws row row_base + r). Lane (j, n) holds row row0 + 16t + n,
+// d = VW (4j + e) + i.
+template <class E, int D, int NT, bool BLK = false>
 __device__ __forceinline__ void write_rows(const WaveState<D, NT>& s, const PAParams& p, const SeqView& sv, int R,
                                            int row0, int kvh, bool partial, float* ws_acc, float* ws_ml,
-                                           int64_t row_base) {
+                                           int64_t row_base, int cap) {
   constexpr int VW = D / 16;
   const int lane = threadIdx.x & 63;
   const int j = lane >> 4, n = lane & 15;
@@ -641,13 +663,26 @@ __device__ __forceinline__ void write_rows(const WaveState<D, NT>& s, const PAPa
       }
     } else {
       const int64_t idx = row_base + r;
-      float* dst = ws_acc + idx * D;
+      if constexpr (BLK) {
+        // part_ofs with the tile t and its row count m uniform: float4 k of this lane at
+        // lp + k 16 m floats (row0 = 0 in every partial write)
+        const int m = min(16, cap - 16 * t);
+        float* lp = ws_acc + (row_base + 16 * t) * D + (j * m + n) * 4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
+        for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int i = 0; i < VW; i += 4)
-          *(f32x4*)(dst + VW * (4 * j + e) + i) =
-              f32x4{s.acc[t][i][e], s.acc[t][i + 1][e], s.acc[t][i + 2][e], s.acc[t][i + 3][e]};
+          for (int i = 0; i < VW; i += 4)
+            *(f32x4*)(lp + (e * (VW / 4) + i / 4) * 16 * m) =
+                f32x4{s.acc[t][i][e], s.acc[t][i + 1][e], s.acc[t][i + 2][e], s.acc[t][i + 3][e]};
+      } else {
+        float* dst = ws_acc + idx * D;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int i = 0; i < VW; i += 4)
+            *(f32x4*)(dst + VW * (4 * j + e) + i) =
+                f32x4{s.acc[t][i][e], s.acc[t][i + 1][e], s.acc[t][i + 2][e], s.acc[t][i + 3][e]};
+      }
       if (j == 0) {
         ws_ml[idx * 2] = s.m[t];
         ws_ml[idx * 2 + 1] = L;
@@ -1068,7 +1103,7 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
                                           (int)(y - seg_beg) * kChunk, L);
       SeqView none{};
       write_rows<E, D, NX>(st, p, none, 16 * NX, 0, kvh, true, p.ws_xacc, p.ws_xml,
-                           ((pseg + unit) * p.HGW + hw) * (16 * NX));
+                           ((pseg + unit) * p.HGW + hw) * (16 * NX), 16 * NX);
       pos = y;
     }
   }
@@ -1110,7 +1145,8 @@ __global__ __launch_bounds__(256) void pa_decode_kernel(PAParams p) {
     run_chunks<E, D, NT, KV8>(st, p, btrow, kvh, tok_lo, kChunk, tok_hi, sv.kv_total);
     const bool whole = pos == seg_beg && y == seg_end && !member;
     const int64_t slot = (int64_t)seq * NHG + hg + unit;
-    write_rows<E, D, NT>(st, p, sv, R, 0, kvh, !whole, p.ws_acc, p.ws_ml, (slot * p.HGW + hw) * p.RS);
+    write_rows<E, D, NT, (KV8 && NT > 1)>(st, p, sv, R, 0, kvh, !whole, p.ws_acc, p.ws_ml, (slot * p.HGW + hw) * p.RS,
+                                         p.RS);
     if (L > 0) {
       if (hw == 0 && lane == 0 && pos == seg_beg) {
         // one record per (seq, hg), written on every call: none for a whole segment; else the
@@ -1192,7 +1228,7 @@ __global__ __launch_bounds__(256) void pa_decode_short_kernel(PAParams p) {
     for (int i = 0; i < NI; ++i) st.acc[0][i] += ak * x_acc[k][i][lane];
   }
   st.m[0] = M;
-  write_rows<E, D, 1>(st, p, sv, R, 0, kvh, false, nullptr, nullptr, 0);
+  write_rows<E, D, 1>(st, p, sv, R, 0, kvh, false, nullptr, nullptr, 0, 16);
 }
 
 // Log-sum-exp merge of split segments. A job covers `rows` partial rows per piece (HGW
@@ -1219,7 +1255,8 @@ constexpr int merge_rows_decode() {
 
 // One workgroup's share of a merge job: rows MR = F * 1024 / D of it (chunk), F float4 of
 // one row per thread.
-template <class E, int D, int F>
+// BLK: decode and prefix pieces in the tile-block layout (launches over E4M3 caches).
+template <class E, int D, int F, bool BLK>
 __device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job, int chunk, bool casc) {
   constexpr int Q4 = D / 4;  // float4 per row
   constexpr int kMergeRows = merge_rows<D, F>();
@@ -1258,6 +1295,17 @@ __device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job,
   int qc[F];
 #pragma unroll
   for (int f = 0; f < F; ++f) qc[f] = min(t + 256 * f, nq - 1);  // clamped: loads stay in the rows
+  // item q -> (row of the workgroup's nr, float4 column): rows fastest for decode and prefix
+  // pieces in the tile-block layout, which holds a column's tile rows in consecutive float4s
+  // (so consecutive threads read consecutive float4s); columns fastest for whole rows
+  auto qrow = [&](int q) {
+    if constexpr (BLK) return dec ? q % nr : q / Q4;
+    return q / Q4;
+  };
+  auto qcol = [&](int q) {
+    if constexpr (BLK) return dec ? q / nr : q % Q4;
+    return q % Q4;
+  };
 
   // Online merge: kMergeBatch pieces at a time, every load of a batch (the m/l pair of each
   // float4's row and the float4) issued before any is used; the running max M moves per batch.
@@ -1274,8 +1322,20 @@ __device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job,
     const float* ap = set ? p.ws_xacc : acc;
     const float* mp = set ? p.ws_xml : ml;
     int64_t rr[F];  // this thread's rows relative to the piece base
+    int64_t ro[F];  // and its float4's float offset from the piece base
 #pragma unroll
-    for (int f = 0; f < F; ++f) rr[f] = roff(set, prow(x0 + qc[f] / Q4));
+    for (int f = 0; f < F; ++f) {
+      rr[f] = roff(set, prow(x0 + qrow(qc[f])));
+      const int c4 = qcol(qc[f]);
+      ro[f] = rr[f] * D + 4 * c4;
+      if constexpr (BLK) {
+        if (dec) {  // decode and prefix pieces: per-head groups of cap rows
+          const int cap = set ? p.XR : p.RS;
+          const int rh = (int)(rr[f] % cap);
+          ro[f] = (rr[f] - rh) * D + part_ofs<D>(rh, c4, cap);
+        }
+      }
+    }
     auto batch = [&](int i0, auto kb) {
       constexpr int KB = decltype(kb)::value;
       float2 mv[KB][F];
@@ -1286,7 +1346,10 @@ __device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job,
 #pragma unroll
         for (int f = 0; f < F; ++f) {
           mv[k][f] = *(const float2*)(mp + (bk + rr[f]) * 2);
-          av[k][f] = *(const f32x4*)(ap + (bk + rr[f]) * D + 4 * (qc[f] % Q4));
+          if constexpr (BLK)
+            av[k][f] = *(const f32x4*)(ap + bk * D + ro[f]);
+          else
+            av[k][f] = *(const f32x4*)(ap + (bk + rr[f]) * D + 4 * (qc[f] % Q4));
         }
       }
 #pragma unroll
@@ -1330,7 +1393,7 @@ __device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job,
   for (int f = 0; f < F; ++f) {
     const int q = t + 256 * f;
     if (q >= nq) continue;
-    const int xr = q / Q4, col = 4 * (q % Q4);
+    const int xr = qrow(q), col = 4 * qcol(q);
     const int x = prow(x0 + xr);
     const int hw = x / rph, r = rbase + x % rph;
     const float inv = p.v_scale / (Ls[f] == 0.f ? 1.f : Ls[f]);
@@ -1341,7 +1404,7 @@ __device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job,
 
 // MIXED: the batch has prefill-class sequences (prefill records after the decode units);
 // decode and prefill jobs then both take 2 float4 per thread (16 rows at D = 128).
-template <class E, int D, bool MIXED>
+template <class E, int D, bool MIXED, bool BLK>
 __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
   constexpr int F = MIXED ? 2 : 1;
   constexpr int MR = merge_rows<D, F>();
@@ -1370,7 +1433,7 @@ __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
     job = p.ws_job + ((int64_t)kMaxDecodeWaves + bp / (p.PR / MR)) * kJobInts;
     chunk = bp % (p.PR / MR);
   }
-  merge_job<E, D, F>(p, job, chunk, casc);
+  merge_job<E, D, F, BLK>(p, job, chunk, casc);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -2401,10 +2464,14 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipSt
   const int cd = (p.HGW * p.RS + mr - 1) / mr;
   const int nseg = plan.cascade ? p.B * (p.Hkv / p.HGW) : 0;  // cascade records
   const dim3 mg((p.NU > nseg ? p.NU : nseg) * cd + p.NUP * (p.PR / merge_rows<D, 2>()));
+  // the partials' layout: tile blocks where the decode kernel wrote them so (write_rows<...,
+  // KV8 && NT > 1>: multi-tile rows over E4M3 caches), whole rows otherwise
   if (plan.launch_prefill)
-    hipLaunchKernelGGL((pa_merge_kernel<E, D, true>), mg, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((pa_merge_kernel<E, D, true, false>), mg, dim3(256), 0, s, p);
+  else if (KV8 && plan.NT > 1)
+    hipLaunchKernelGGL((pa_merge_kernel<E, D, false, true>), mg, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((pa_merge_kernel<E, D, false>), mg, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((pa_merge_kernel<E, D, false, false>), mg, dim3(256), 0, s, p);
   if ((err = (int)hipGetLastError())) return err;
   log.after_launch(3, s);
   return 0;
