@@ -185,6 +185,30 @@ def test_split_decode_segments(hip_device):
     assert err <= pc.TOL_16BIT, err
 
 
+@pytest.mark.parametrize("idx", [2, 4, 5])
+def test_baseline_configs_fp8(hip_device, idx):
+    """BASELINE configs 2, 4 and 5 at full size over E4M3 caches: the single-tile decode with
+    two dispatch rounds, the 32-row cascade groups, and the two-tile verify rows whose split
+    pieces keep their partials in tile blocks. Any E4M3 content will do (the caches are cast on
+    the device); the fp64 oracle reads the dequantized caches after the step's write, over
+    sampled sequences."""
+    w = workloads.baseline_config(idx, seed=0)
+    b = workloads.materialize(w, torch.bfloat16, hip_device, seed=idx)
+    ks, vs = 0.5, 2.0
+    kc = (b.k_cache.float() / ks).clamp(-fp8.FP8_MAX, fp8.FP8_MAX).to(torch.float8_e4m3fn)
+    vc = (b.v_cache.float() / vs).clamp(-fp8.FP8_MAX, fp8.FP8_MAX).to(torch.float8_e4m3fn)
+    out = _attend_fp8(b, kc, vc, ks, vs)
+    kinds = last_launch_kernels()
+    torch.cuda.synchronize()
+    assert kinds == (["share", "decode", "reduce"] if idx == 4 else ["decode", "reduce"]), kinds
+    assert torch.isfinite(out.float()).all()
+    deq = dataclasses.replace(b, k_cache=fp8.dequantize(kc, ks), v_cache=fp8.dequantize(vc, vs))
+    seqs = list(range(0, len(w.query_lens), 4 if idx == 2 else 1))
+    err = pc.max_err_vs_oracle(deq, out, seqs)
+    print(f"config {idx} over E4M3: max abs err vs fp64 oracle {err:.3e}")
+    assert err <= pc.TOL_16BIT, err
+
+
 def test_partial_second_dispatch_round(hip_device):
     """Tables 4096 keys wide over contexts of 120-260 tokens: the decode launch is sized from
     the tables for two workgroups per CU (256 units, the first 128 in the first dispatch round),
