@@ -27,7 +27,8 @@ Also printed in the same JSON line:
   cpu_baseline - the torch restatement of the reference's TorchAttention.forward (fp32, the
                  host's cores) on a bounded sample of the same workload;
   secondary    - the other BASELINE configs (C1, C3 prefill TFLOP/s + decode GB/s, C4 on
-                 unique bytes, C5), timed the same way with fewer steps;
+                 unique bytes, C5), and C2-C5 over E4M3 caches, timed the same way with
+                 fewer steps;
   metadata_prep - per-step input preparation at C2 and C3: the reference's host path vs
                  block tables resident on the device (kvh_prepare_metadata);
   engine_decode_tok_s - Llama-3.2-1B / Llama-3.1-8B decode tokens/s of the engine harness
@@ -736,7 +737,7 @@ def main() -> int:
         print(f"# traffic: {t}", file=sys.stderr, flush=True)
     if not args.no_secondary:
         sec = {}
-        runs = [(idx, False) for idx in (1, 3, 4, 5)] + [(idx, True) for idx in (2, 3, 4)]
+        runs = [(idx, False) for idx in (1, 3, 4, 5)] + [(idx, True) for idx in (2, 3, 4, 5)]
         for idx, kv8 in runs:
             r = measure(idx, max(20, args.steps), 3, max(10, args.prof_iters), fp8=kv8)
             print(f"# c{idx}{' fp8 kv' if kv8 else ''}: {r}", file=sys.stderr, flush=True)
