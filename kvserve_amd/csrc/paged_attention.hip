@@ -615,17 +615,16 @@ __device__ __forceinline__ SeqView seq_view_uniform(const PAParams& p, int seq) 
 
 // Float offset of float4 c4 of row r in a head's group of `cap` partial rows (one split
 // piece's fp32 accumulators, written by write_rows, read by the merge) in the tile-block
-// layout (launches over E4M3 caches: write_rows<..., BLK> and merge_job<..., BLK>). The rows
-// are kept in 16-row tiles in the order the accumulator lanes hold them: lane (j, n) of a tile
-// holds row n, d = VW (4j + e) + i, i.e. float4 c4 = VW j + k with k = e VW / 4 + i / 4, and
-// that float4 lies at
-// (k * 4 + j) * m + n of the tile's m-row block (m = min(16, cap - 16 t)). Each store
-// instruction of a wave (one k) then writes 64 m contiguous bytes; with rows laid out whole it
-// writes 16 bytes to each of 4 lines of every row. HBM-cold, three runs each: C5 over E4M3
-// (two row tiles) decode 58.2 -> 50.3 us, merge 10.8 -> 11.9; single-tile rows over E4M3 (C2,
-// C4) gained 0.3-0.6 us in the decode kernel and lost 0.6-1.3 us in the merge, and over
-// 16-bit caches the decode kernels gained at most 0.8 us and the merges lost up to 1.0, so
-// those keep whole rows: the layout is used by multi-tile rows over E4M3 caches only.
+// layout (multi-tile rows over E4M3 caches: write_rows<..., BLK> and merge_job<..., BLK>). The
+// rows are kept in 16-row tiles in the order the accumulator lanes hold them: lane (j, n) of
+// a tile holds row n, d = VW (4j + e) + i, i.e. float4 c4 = VW j + k with k = e VW / 4 + i / 4,
+// and that float4 lies at (k * 4 + j) * m + n of the tile's m-row block (m = min(16, cap -
+// 16 t)). Each store instruction of a wave (one k) then writes 64 m contiguous bytes; with rows
+// laid out whole it writes 16 bytes to each of 4 lines of every row. HBM-cold, three runs
+// each: C5 over E4M3 (two row tiles) decode 58.9 -> 51.3 us, merge 11.1 -> 12.1; single-tile
+// rows over E4M3 (C2, C4) gained 0.3-0.6 us in the decode kernel and lost 0.6-1.3 us in the
+// merge, and over 16-bit caches the decode kernels gained at most 0.8 us and the merges lost
+// up to 1.0, so those keep whole rows.
 template <int D>
 __device__ __forceinline__ int part_ofs(int r, int c4, int cap) {
   constexpr int VW = D / 16;
@@ -1255,7 +1254,8 @@ constexpr int merge_rows_decode() {
 
 // One workgroup's share of a merge job: rows MR = F * 1024 / D of it (chunk), F float4 of
 // one row per thread.
-// BLK: decode and prefix pieces in the tile-block layout (launches over E4M3 caches).
+// BLK: the decode pieces are in the tile-block layout (multi-tile rows over E4M3 caches, never
+// with a cascade prefix).
 template <class E, int D, int F, bool BLK>
 __device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job, int chunk, bool casc) {
   constexpr int Q4 = D / 4;  // float4 per row
@@ -1295,9 +1295,9 @@ __device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job,
   int qc[F];
 #pragma unroll
   for (int f = 0; f < F; ++f) qc[f] = min(t + 256 * f, nq - 1);  // clamped: loads stay in the rows
-  // item q -> (row of the workgroup's nr, float4 column): rows fastest for decode and prefix
-  // pieces in the tile-block layout, which holds a column's tile rows in consecutive float4s
-  // (so consecutive threads read consecutive float4s); columns fastest for whole rows
+  // item q -> (row of the workgroup's nr, float4 column): rows fastest for decode pieces in
+  // the tile-block layout, which holds a column's tile rows in consecutive float4s (so
+  // consecutive threads read consecutive float4s); columns fastest for whole rows
   auto qrow = [&](int q) {
     if constexpr (BLK) return dec ? q % nr : q / Q4;
     return q / Q4;
@@ -1329,7 +1329,7 @@ __device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job,
       const int c4 = qcol(qc[f]);
       ro[f] = rr[f] * D + 4 * c4;
       if constexpr (BLK) {
-        if (dec) {  // decode and prefix pieces: per-head groups of cap rows
+        if (dec) {  // decode pieces: per-head groups of cap rows
           const int cap = set ? p.XR : p.RS;
           const int rh = (int)(rr[f] % cap);
           ro[f] = (rr[f] - rh) * D + part_ofs<D>(rh, c4, cap);
