@@ -1245,11 +1245,13 @@ constexpr int merge_rows() {
   return F * 256 * 4 / D;
 }
 
-// F = 1 in decode-only batches; in mixed batches F = 2, since there a head's RS = 16 / G row
-// slots mostly hold a single query's G rows and the workgroups past them return at once
+// F = 1 in decode-only batches; in mixed batches F = 4, since there a head's RS = 16 / G row
+// slots mostly hold a single query's G rows and the workgroups past them return at once, and
+// a prefill tile's rows merge from 2-3 pieces each, so a thread keeps more loads in flight
+// with more float4 (C3, HBM-cold, three runs each: merge 24.7 -> 23.0 us against F = 2)
 template <int D, bool MIXED>
 constexpr int merge_rows_decode() {
-  return MIXED ? merge_rows<D, 2>() : merge_rows<D, 1>();
+  return MIXED ? merge_rows<D, 4>() : merge_rows<D, 1>();
 }
 
 // One workgroup's share of a merge job: rows MR = F * 1024 / D of it (chunk), F float4 of
@@ -1406,8 +1408,11 @@ __device__ __forceinline__ void merge_job(const PAParams& p, const int32_t* job,
 // decode and prefill jobs then both take 2 float4 per thread (16 rows at D = 128).
 template <class E, int D, bool MIXED, bool BLK>
 __global__ __launch_bounds__(256) void pa_merge_kernel(PAParams p) {
-  constexpr int F = MIXED ? 2 : 1;
+  constexpr int F = MIXED ? 4 : 1;
   constexpr int MR = merge_rows<D, F>();
+  static_assert(!MIXED || ((kWavesPerWG * 16 * prefill_nt<false>()) % MR == 0 &&
+                           (kWavesPerWG * 16 * prefill_nt<true>()) % MR == 0),
+                "a prefill tile's rows split into whole merge chunks");
   const int CD = (p.HGW * p.RS + MR - 1) / MR;
   const int b = blockIdx.x;
   const int32_t* job;
@@ -2463,7 +2468,7 @@ static int launch_mfma_typed(PAParams& p, const Plan& plan, int32_t max_q, hipSt
   const int mr = plan.launch_prefill ? merge_rows_decode<D, true>() : merge_rows_decode<D, false>();
   const int cd = (p.HGW * p.RS + mr - 1) / mr;
   const int nseg = plan.cascade ? p.B * (p.Hkv / p.HGW) : 0;  // cascade records
-  const dim3 mg((p.NU > nseg ? p.NU : nseg) * cd + p.NUP * (p.PR / merge_rows<D, 2>()));
+  const dim3 mg((p.NU > nseg ? p.NU : nseg) * cd + p.NUP * (p.PR / merge_rows<D, 4>()));
   // the partials' layout: tile blocks where the decode kernel wrote them so (write_rows<...,
   // KV8 && NT > 1>: multi-tile rows over E4M3 caches), whole rows otherwise
   if (plan.launch_prefill)
