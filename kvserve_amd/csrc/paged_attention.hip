@@ -1232,14 +1232,15 @@ __global__ __launch_bounds__(256) void pa_decode_short_kernel(PAParams p) {
 
 // Log-sum-exp merge of split segments. A job covers `rows` partial rows per piece (HGW
 // heads x RS rows for decode, PAParams::PR rows of one head for prefill); row x of piece i
-// sits at (slot(i) * rows + x) in the partial arrays. Each workgroup merges MR = 1024 / D
-// rows of one job: workgroups 0 .. NU * CD - 1 take decode unit b / CD, rows MR (b % CD) ..;
-// the next NUP * (128 / MR) take prefill record b' / (128 / MR), rows MR (b' % (128 / MR)) ...
-// Every thread owns one float4 of the MR rows and merges it online over the pieces,
-// kMergeBatch pieces per round of loads. Rows are normalised at the store.
+// sits at (slot(i) * rows + x) in the partial arrays (whole rows; decode pieces of multi-tile
+// rows over E4M3 caches in the tile-block layout of part_ofs). Each workgroup merges
+// MR = F 1024 / D rows of one job: workgroups 0 .. NU * CD - 1 take decode unit b / CD, rows
+// MR (b % CD) ..; the next NUP * (PR / MR) take prefill record b' / (PR / MR), rows
+// MR (b' % (PR / MR)) ... Every thread owns F float4 of the MR rows and merges them online
+// over the pieces, kMergeBatch / F pieces per round of loads. Rows are normalised at the store.
 constexpr int kMergeBatch = 16;
-// rows per merge workgroup with F float4 of one row per thread: F 1024 / D (decode jobs
-// F = 1: 8 rows at D = 128; prefill jobs F = 2: 16 rows)
+// rows per merge workgroup with F float4 of one row per thread: F 1024 / D (decode-only
+// batches F = 1: 8 rows at D = 128; mixed batches F = 4: 32 rows)
 template <int D, int F = 1>
 constexpr int merge_rows() {
   return F * 256 * 4 / D;
