@@ -582,6 +582,51 @@ def test_prefill_priority_change_points_match_the_per_chunk_level():
                     assert lvl == lvl_of(i, n, rest, total), (total, n, rest, i)
 
 
+def test_partial_tile_block_layout():
+    """The tile-block layout of split-piece partials (multi-tile rows over E4M3 caches):
+    `part_ofs`, which the merge reads by, must place a head group's cap rows x D floats as a
+    permutation of [0, cap D) in whole float4s, and the writer's store address (lane (j, n) of
+    tile t, float4 k of its accumulator row: lp + k 16 m) must be part_ofs of that lane's row
+    and column, for every cap a launch uses (RS = q_len G rows) at both MFMA head sizes. The
+    expressions are taken from the source."""
+    src = (Path(__file__).resolve().parent.parent / "kvserve_amd/csrc/paged_attention.hip").read_text()
+    body = re.search(r"int part_ofs\(int r, int c4, int cap\) \{(.*?)\n\}", src, re.S).group(1)
+    tnm = re.search(r"const int t = (.*?), n = (.*?), m = (.*?);", body)
+    ret = re.search(r"return (.*?);", body).group(1)
+    lp = re.search(r"float\* lp = ws_acc \+ (.*?);", src).group(1)
+    st = re.search(r"\*\(f32x4\*\)\(lp \+ (.*?)\) =", src).group(1)
+
+    def cdiv(e):  # C integer expressions on non-negative ints -> Python (>>, &, min carry over)
+        return e.replace("/", "//")
+
+    def part_ofs(r, c4, cap, D):
+        VW = D // 16
+        env = {"r": r, "c4": c4, "cap": cap, "D": D, "VW": VW, "min": min}
+        env["t"] = eval(cdiv(tnm.group(1)), env)  # noqa: S307 (source text of this repo)
+        env["n"] = eval(cdiv(tnm.group(2)), env)  # noqa: S307
+        env["m"] = eval(cdiv(tnm.group(3)), env)  # noqa: S307
+        return eval(cdiv(ret), env)  # noqa: S307
+
+    for D in (64, 128):
+        VW = D // 16
+        for cap in (16, 20, 24, 32, 48, 64, 12, 4):
+            offs = {part_ofs(r, c4, cap, D) for r in range(cap) for c4 in range(D // 4)}
+            assert len(offs) == cap * D // 4 and offs == set(range(0, cap * D, 4)), (D, cap)
+            for t in range((cap + 15) // 16):
+                m = min(16, cap - 16 * t)
+                for j in range(4):
+                    for n in range(m):
+                        env = {"row_base": 0, "t": t, "D": D, "j": j, "m": m, "n": n, "VW": VW}
+                        base = eval(cdiv(lp), env)  # noqa: S307
+                        for e in range(4):
+                            for i in range(0, VW, 4):
+                                env.update(e=e, i=i)
+                                got = base + eval(cdiv(st), env)  # noqa: S307
+                                # lane (j, n) holds d = VW (4 j + e) + i .. + 3 of row 16 t + n
+                                c4 = (VW * (4 * j + e) + i) // 4
+                                assert got == part_ofs(16 * t + n, c4, cap, D), (D, cap, t, j, n, e, i)
+
+
 def test_decode_cost_split_partitions_the_positions():
     """The decode kernel's stream-K split (`CostSplit`: the first P positions cost wp, the others
     wr; the first R1 units take K1 parts of the total cost, the others K2) must give every
